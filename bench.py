@@ -1,0 +1,194 @@
+"""Benchmark of the PECO per-layer attention hot path on one MI355X.
+
+One step = one PecoAttention.attention call (sparse path) on the HunyuanVideo 480x720x17f
+layer: 24 heads, 6750 video + 256 text tokens, D=128, bf16, k-means with 64 Q / 256 K
+clusters and 10 Lloyd iterations from explicit initial centroids, 25% of key clusters
+kept, Base-Offset off (``--workload hunyuan_480p_bo4`` turns it on). Inputs are
+synthetic (Gaussian mixtures) and resident in HBM before timing starts.
+
+value = effective TFLOP/s = 4*D*sum(kept |Q_i||K_j|) / layer time, the reference's metric.
+The roofline object reports the attention kernel (the dominant MFMA kernel): its
+algorithmic FLOPs over its average duration measured with events on the launch stream.
+cpu_baseline times the oracle's restatement of the reference CPU torch path on a bounded
+sample of heads of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "PECO attn-layer ms + effective TFLOP/s at 24h x 7k tok bf16; % MFMA/HBM peak"
+PEAK_BF16_TFLOPS = 2516.6
+PEAK_HBM_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="hunyuan_480p")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--stage-reps", type=int, default=10)
+    return ap.parse_args()
+
+
+def make_layer(wl):
+    from peco_amd import processor
+
+    s = wl.shape
+    cfg = processor.PecoConfig(num_q_centroids=s.num_q_centroids, num_k_centroids=s.num_k_centroids, top_p=wl.top_p,
+                               min_kc_ratio=wl.min_kc_ratio, kmeans_iter_init=s.iterations,
+                               kmeans_iter_step=s.iterations, warmup_steps=0, base_offset_bits=s.bits)
+    ctx = processor.InferenceContext(step=0, text_length=s.text, valid_text_length=s.text)
+    return processor.PecoAttention(0, cfg, ctx)
+
+
+def run_step(layer, wl, q, k, v, q_init, k_init):
+    # Every step fits from the same explicit initial centroids (the workload's k-means spec).
+    layer.q_centroids, layer.k_centroids = q_init, k_init
+    return layer.attention(q, k, v)
+
+
+def stage_breakdown(layer, wl, q, k, v, q_init, k_init, reps):
+    """Per-stage device time (ms) with events on the current stream, and the realised FLOPs."""
+    from peco_amd import attention_cuda, clustering_cuda, processor, workloads
+    from peco_amd.clustering import select_cluster_connections
+
+    s = wl.shape
+    n, length, dim, heads = s.video, s.length, s.dims, s.heads
+    names = ("kmeans", "select", "pack", "partition", "attention")
+    acc = {k_: 0.0 for k_ in names}
+    flops = 0.0
+    for _ in range(reps):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+        ev[0].record()
+        layer.q_centroids, layer.k_centroids = q_init, k_init
+        ql, kl, qs, ks = layer._update_cluster_state(q[:, :, :n], k[:, :, :n])
+        q_idx, k_idx = layer._last_fit
+        ev[1].record()
+        dmap = select_cluster_connections(layer.q_centroids.reshape(1, heads, -1, dim),
+                                          layer.k_centroids.reshape(1, heads, -1, dim), qs, ks, wl.top_p,
+                                          wl.min_kc_ratio)
+        ev[2].record()
+        qp, kp, vp = clustering_cuda.pack_clustered([q, k, v], [q_idx, k_idx, k_idx], [ql, kl, None],
+                                                    [layer.q_centroids, layer.k_centroids, None], [s.bits, s.bits, 0],
+                                                    n)
+        ev[3].record()
+        emap, eqs, eks = processor._extend_partition_on_device(dmap, qs, ks, s.text, s.text)
+        idx = torch.empty((heads, length), dtype=torch.int32, device=q.device)
+        idx[:, :n] = q_idx
+        idx[:, n:] = torch.arange(n, length, device=q.device, dtype=torch.int32)
+        ev[4].record()
+        attention_cuda.sparse_attention(qp, kp, vp, emap, eqs, eks, validate_sizes=False, out_index=idx)
+        ev[5].record()
+        torch.cuda.synchronize()
+        for i, nm in enumerate(names):
+            acc[nm] += ev[i].elapsed_time(ev[i + 1])
+        flops = workloads.attention_flops(emap, eqs, eks, dim)
+    return {k_: v_ / reps for k_, v_ in acc.items()}, flops, (qp, kp, vp, emap, eqs, eks, idx)
+
+
+def attention_kernel_time(args_, reps=20):
+    """Average duration of the sparse-attention launch (builder + kernel) on its stream."""
+    from peco_amd import attention_cuda
+
+    qp, kp, vp, emap, eqs, eks, idx = args_
+    for _ in range(3):
+        attention_cuda.sparse_attention(qp, kp, vp, emap, eqs, eks, validate_sizes=False, out_index=idx)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        attention_cuda.sparse_attention(qp, kp, vp, emap, eqs, eks, validate_sizes=False, out_index=idx)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def cpu_baseline(wl, budget_s):
+    """Oracle (reference CPU torch path) on whole heads of the workload until the budget is spent."""
+    from oracle import reference_path
+    from peco_amd import workloads
+
+    s = wl.shape
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    n = s.video
+    done, flops, elapsed = 0, 0.0, 0.0
+    while done < s.heads and (elapsed < budget_s or done == 0):
+        h = slice(done, done + 1)
+        q, k, v = (t[:, h].cpu().contiguous() for t in (wl.query, wl.key, wl.value))
+        stages = {}
+        t0 = time.perf_counter()
+        reference_path.peco_layer(q, k, v, num_q_centroids=s.num_q_centroids, num_k_centroids=s.num_k_centroids,
+                                  iterations=s.iterations, q_init=wl.q_init[h].cpu(), k_init=wl.k_init[h].cpu(),
+                                  top_p=wl.top_p, min_kc_ratio=wl.min_kc_ratio, bits=s.bits, text_length=s.text,
+                                  valid_text=s.text, stages=stages)
+        elapsed += time.perf_counter() - t0
+        flops += workloads.attention_flops(stages["ext_map"], stages["ext_q_sizes"], stages["ext_k_sizes"], s.dims)
+        done += 1
+    return {"value": flops / elapsed / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{done} of {s.heads} heads of {s.name}, full sequence, oracle reference_path "
+                      f"(torch CPU, {threads} threads); {elapsed:.2f} s; "
+                      f"layer {1e3 * elapsed / done * s.heads:.1f} ms extrapolated to {s.heads} heads"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are not part of it",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    from peco_amd import workloads
+
+    dev = torch.device("cuda:0")
+    wl = workloads.make_workload(args.workload, device=dev)
+    s = wl.shape
+    layer = make_layer(wl)
+    q, k, v = wl.query, wl.key, wl.value
+    q_init, k_init = wl.q_init, wl.k_init
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            run_step(layer, wl, q, k, v, q_init, k_init)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            run_step(layer, wl, q, k, v, q_init, k_init)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / args.steps
+        stages, flops, attn_args = stage_breakdown(layer, wl, q, k, v, q_init, k_init, args.stage_reps)
+        t_attn = attention_kernel_time(attn_args)
+    value = flops / (ms * 1e-3) / 1e12
+    achieved = flops / (t_attn * 1e-3) / 1e12
+    line = {
+        "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": s.name, "heads": s.heads, "video_tokens": s.video, "text_tokens": s.text,
+                   "head_dim": s.dims, "q_clusters": s.num_q_centroids, "k_clusters": s.num_k_centroids,
+                   "kmeans_iterations": s.iterations, "keep_ratio": s.keep_ratio, "base_offset_bits": s.bits},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "kernel": "sparse_attention (work list + MFMA kernel)", "kernel_ms": round(t_attn, 4),
+                     "flops": flops},
+        "stages_ms": {k_: round(v_, 4) for k_, v_ in stages.items()},
+        "layer_frac_of_peak": round(value / PEAK_BF16_TFLOPS, 4),
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,118 @@
+/*
+ * C-ABI of libpeco_hip.so: the PECO per-layer attention hot path on MI355X (gfx950).
+ *
+ * Conventions (same as the reference's two CUDA libraries):
+ *   - every pointer is device memory owned by the caller, unless stated otherwise;
+ *   - every call is asynchronous on `stream` (a hipStream_t; torch's current stream);
+ *   - return 0 on success, a hipError_t value on a runtime error, 1 (hipErrorInvalidValue)
+ *     on bad arguments, or a PECO status >= 20001 (see peco_cluster_error_message).
+ * dtype codes: 0 = fp16, 1 = bf16, 2 = fp32.
+ */
+#ifndef PECO_HIP_H
+#define PECO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- Reference ABI: peco/kernels/kmeans.cu (bound by peco/clustering_cuda.py:65-71) ---- */
+
+/* Replaces peco_assign_tokens_to_centers, peco/kernels/kmeans.cu:139.
+ * labels[b,t] = argmin_j fma(-2, x_t.c_j, |c_j|^2), lowest j on ties (fixed-order fp32).
+ * center_norms (nullable) receives |c_j|^2. scratch/chunk_size are accepted and unused. */
+int peco_assign_tokens_to_centers(const float* x, const float* centers, int32_t* labels, float* scratch,
+                                  float* center_norms, int batch, int tokens, int dims, int clusters,
+                                  int chunk_size, void* stream);
+
+/* Replaces peco_recompute_cluster_centers, peco/kernels/kmeans.cu:179.
+ * sums (nullable) / counts / means of x rows per label; sums accumulate in token order;
+ * an empty cluster keeps `previous`. */
+int peco_recompute_cluster_centers(const float* x, const int32_t* labels, const float* previous, float* sums,
+                                   int32_t* counts, float* means, int batch, int tokens, int dims, int clusters,
+                                   void* stream);
+
+/* Replaces peco_reorder_token_features, peco/kernels/kmeans.cu:200.
+ * inverse=0: out[b,j] = in[b, indices[b,j]]; inverse=1: out[b, indices[b,j]] = in[b,j].
+ * item_size 2 or 4 (bit copy of fp16/bf16/fp32 rows). */
+int peco_reorder_token_features(const void* input, const int32_t* indices, void* output, int batch_heads,
+                                int tokens, int dims, int item_size, int inverse, void* stream);
+
+/* Replaces peco_cluster_error_message, peco/kernels/kmeans.cu:220. Static string. */
+const char* peco_cluster_error_message(int code);
+
+/* ---- Reference ABI: peco/kernels/sparse_attention.cu (bound by peco/attention_cuda.py:57-60) ---- */
+
+/* Replaces peco_sparse_attention, peco/kernels/sparse_attention.cu:210.
+ * q [bh,sq,d], k/v [bh,sk,d] (fp16/bf16, d in {64,128}), selected bool [bh,cq,ck],
+ * int32 sizes [bh,cq]/[bh,ck]; workspace holds bh*(ck+2+3*(ceil(sq/16)+cq)) int32
+ * (the reference's own size). Fully masked rows are zero. */
+int peco_sparse_attention(const void* q, const void* k, const void* v, const uint8_t* selected,
+                          const int* q_sizes, const int* k_sizes, void* output, int* workspace, int bh, int sq,
+                          int sk, int d, int cq, int ck, int dtype, void* stream);
+
+/* Replaces peco_attention_error_string, peco/kernels/sparse_attention.cu:232. */
+const char* peco_attention_error_string(int code);
+
+/* ---- Extensions (no counterpart in the reference's native code) ---- */
+
+/* ABI revision of this library. */
+int peco_abi_version(void);
+
+/* Stable argsort of labels per batch entry as a counting sort (replaces the torch.argsort
+ * of peco/clustering.py:105). indices[b,j] = original token at sorted position j;
+ * ranks (nullable) = inverse permutation; counts (nullable) [b,clusters];
+ * offsets (nullable) [b,clusters+1]. clusters <= 16384. */
+size_t peco_cluster_sort_workspace_size(int batch, int tokens, int clusters);
+int peco_cluster_sort(const int32_t* labels, int batch, int tokens, int clusters, int32_t* indices, int32_t* ranks,
+                      int32_t* counts, int32_t* offsets, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Fused Lloyd fit (peco/clustering.py:17-89 with tol=0) of num_problems (1 or 2)
+ * independent problems sharing every launch. Problem i: x[i] rows [batch, tokens, dims]
+ * in `dtype` with batch stride x_batch_stride[i] elements (NULL or 0 = tokens*dims),
+ * initial centres centers_in[i] fp32 [batch, clusters, dims]; outputs centers_out[i],
+ * labels[i] [batch,tokens], counts[i] [batch,clusters], sorted_indices[i] (stable sort
+ * of the final labels) and offsets[i] [batch, clusters+1]. dims in {64, 128}. */
+size_t peco_kmeans_workspace_size(int batch, int tokens, int clusters, int dims);
+int peco_kmeans_fit(int num_problems, const void* const* x, const int64_t* x_batch_stride,
+                    const float* const* centers_in, float* const* centers_out, int32_t* const* labels,
+                    int32_t* const* counts, int32_t* const* sorted_indices, int32_t* const* offsets,
+                    const int* batch, const int* tokens, const int* clusters, int dims, int dtype, int iterations,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* Base-Offset PE quantizer (peco/quantization.py:97-150), dims in {64, 128}.
+ * encode: codes uint8 [batch,tokens,dims] (nullable), low/scale fp32 [batch,tokens] (nullable).
+ * decode: x_hat in `dtype` from codes/low/scale. fake_quant: encode+decode in one pass. */
+int peco_base_offset_encode(const void* x, int dtype, const int32_t* labels, const float* centroids, int batch,
+                            int tokens, int clusters, int dims, int bits, uint8_t* codes, float* low, float* scale,
+                            void* stream);
+int peco_base_offset_decode(const uint8_t* codes, const float* low, const float* scale, const int32_t* labels,
+                            const float* centroids, int batch, int tokens, int clusters, int dims, int dtype,
+                            void* out, void* stream);
+int peco_base_offset_fake_quant(const void* x, int dtype, const int32_t* labels, const float* centroids, int batch,
+                                int tokens, int clusters, int dims, int bits, void* out, void* stream);
+
+/* One launch packing up to 3 tensors [batch, length, dims] (fuses peco/processor.py:141-149):
+ * rows [0, video) in the order of indices[i] [batch, video], fake-quantized against
+ * labels[i]/centroids[i] when bits[i] is 4 or 8; rows [video, length) copied unchanged. */
+int peco_pack_clustered(const void* const* inputs, void* const* outputs, const int32_t* const* indices,
+                        const int32_t* const* labels, const float* const* centroids, const int* clusters,
+                        const int* bits, int num_tensors, int batch, int length, int video, int dims, int dtype,
+                        void* stream);
+
+/* peco_sparse_attention with an explicit workspace size (int32 elements, at least
+ * peco_sparse_attention_workspace_size) and an optional out_index [bh, sq]: output row j
+ * of head b is written to row out_index[b,j] (fuses peco/clustering.py:128-136). */
+size_t peco_sparse_attention_workspace_size(int bh, int sq, int sk, int cq, int ck);
+int peco_sparse_attention_ex(const void* q, const void* k, const void* v, const uint8_t* selected,
+                             const int* q_sizes, const int* k_sizes, void* output, const int32_t* out_index,
+                             int* workspace, size_t workspace_ints, int bh, int sq, int sk, int d, int cq, int ck,
+                             int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PECO_HIP_H */

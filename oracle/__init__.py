@@ -1,0 +1,22 @@
+"""CPU oracle for the PECO per-layer attention hot path.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() and by
+bench.py's cpu_baseline leg, always as the checker. The product package
+(peco_amd) never imports it.
+
+Two layers:
+- ``oracle.canonical``: ctypes wrapper over ``peco_oracle.c``, the fixed-order
+  fp32 restatement the HIP kernels must match bit for bit (k-means assign/update,
+  stable sort, Base-Offset quantizer) plus a double-precision sparse attention.
+- ``oracle.reference_path``: the reference's CPU torch path restated with the
+  same torch operations (clustering.py CPU branches, selection, quantization,
+  processor orchestration, block-sparse CPU attention). It is the CPU baseline
+  that bench.py times, and the pin for the canonical layer.
+
+Parity pins (tests/test_oracle.py): brute-force float64 argmin with near-tie
+certification; torch bmm/scatter_add_/argsort/elementwise ops as library
+routines; closed forms and special cases (constant residual, duplicate
+centroids, empty clusters, p=1, all-true map == SDPA, block-diagonal map ==
+per-cluster SDPA, masked rows == 0); hand-written fixtures for the text
+partition. No function of the oracle is "parity unpinned".
+"""

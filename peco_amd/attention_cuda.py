@@ -1,0 +1,105 @@
+"""Cluster-sparse attention on gfx950 MFMA (peco/attention_cuda.py interface).
+
+QK^T and PV both run on MFMA (v_mfma_f32_32x32x16 bf16/fp16); the online softmax is
+FP32. Unlike the reference, which keeps P in FP32 for a CUDA-core PV product, P is
+rounded to the input dtype before the PV MFMA. Inference only; backward is unsupported.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _native
+
+
+def _device_is_gfx950(device) -> bool:
+    name = getattr(torch.cuda.get_device_properties(device), "gcnArchName", "")
+    return name.split(":")[0] == "gfx950"
+
+
+def _validate(q, k, v, dynamic_map, q_sizes, k_sizes):
+    """Argument checks of peco/attention_cuda.py:84-119 (same messages)."""
+    tensors = (q, k, v, dynamic_map, q_sizes, k_sizes)
+    if not all(isinstance(tensor, torch.Tensor) for tensor in tensors):
+        raise TypeError("All sparse attention inputs must be torch tensors")
+    if q.ndim != 4 or k.ndim != 4 or v.shape != k.shape:
+        raise ValueError("Expected Q [B,H,SQ,D] and equal-shaped K/V [B,H,SK,D]")
+    batch, heads, sq, dim = q.shape
+    if batch < 1 or heads < 1 or batch * heads > 65535:
+        raise ValueError("B*H must be between 1 and 65535")
+    if k.shape[:2] != q.shape[:2] or k.shape[-1] != dim:
+        raise ValueError("Q and K/V batch, head, and feature dimensions must match")
+    if dim not in (64, 128):
+        raise ValueError("HIP attention supports head dimensions 64 and 128")
+    if q.dtype not in (torch.float16, torch.bfloat16) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise TypeError("Q/K/V must share dtype torch.float16 or torch.bfloat16")
+    if not q.is_cuda or any(t.device != q.device for t in tensors):
+        raise ValueError("All sparse attention inputs must reside on the same GPU device")
+    if any(not t.is_contiguous() for t in tensors):
+        raise ValueError("All sparse attention inputs must be contiguous")
+    if q_sizes.ndim != 3 or k_sizes.ndim != 3 or q_sizes.shape[:2] != (batch, heads) or k_sizes.shape[:2] != (batch, heads):
+        raise ValueError("Cluster sizes must have shape [B,H,C]")
+    cq, ck = q_sizes.shape[-1], k_sizes.shape[-1]
+    if cq < 1 or ck < 1 or dynamic_map.shape != (batch, heads, cq, ck):
+        raise ValueError("Expected a nonempty cluster axis and dynamic_map [B,H,CQ,CK]")
+    if dynamic_map.dtype != torch.bool or q_sizes.dtype != torch.int32 or k_sizes.dtype != torch.int32:
+        raise TypeError("dynamic_map must be bool and cluster sizes must be int32")
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
+        raise RuntimeError("PECO HIP sparse attention supports inference only; use torch.no_grad()")
+    sk = k.shape[-2]
+    capacity = (sq + 15) // 16 + cq
+    stride = ck + 2 + 3 * capacity
+    if max(sq, sk, cq, ck, capacity, stride) > 2**31 - 1:
+        raise ValueError("Sequence/cluster metadata exceeds the int32 indexing limit")
+    return batch, heads, sq, dim, sk, cq, ck, stride
+
+
+def sparse_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    dynamic_map: torch.Tensor,
+    q_sizes: torch.Tensor,
+    k_sizes: torch.Tensor,
+    *,
+    validate_sizes: bool = True,
+    out_index: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Return cluster-masked softmax(QK^T/sqrt(D))V.
+
+    Inputs must be contiguous GPU tensors: Q [B,H,SQ,D], K/V [B,H,SK,D], bool map
+    [B,H,CQ,CK] and int32 sizes [B,H,CQ/CK]. Tokens must already be grouped in cluster
+    order. Empty clusters and completely masked rows are supported; a completely masked
+    row returns zero. Sizes are checked on the stream without copying them to the host.
+    ``out_index`` (int32 [B*H, SQ], optional) writes output row j of head b to row
+    out_index[b, j] instead, fusing the inverse token permutation into the epilogue.
+    """
+    batch, heads, sq, dim, sk, cq, ck, stride = _validate(q, k, v, dynamic_map, q_sizes, k_sizes)
+    with torch.cuda.device(q.device):
+        if not _device_is_gfx950(q.device):
+            raise RuntimeError("This HIP build requires an MI355X-class gfx950 GPU")
+        if validate_sizes:
+            torch._assert_async((q_sizes >= 0).all(), "q_sizes must be nonnegative")
+            torch._assert_async((k_sizes >= 0).all(), "k_sizes must be nonnegative")
+            torch._assert_async((q_sizes.sum(-1) == sq).all(), "q_sizes must sum to the Q sequence length")
+            torch._assert_async((k_sizes.sum(-1) == sk).all(), "k_sizes must sum to the K sequence length")
+        output = torch.empty_like(q)
+        if sq == 0:
+            return output
+        if out_index is not None:
+            if out_index.dtype != torch.int32 or out_index.numel() != batch * heads * sq or not out_index.is_contiguous():
+                raise ValueError("out_index must be a contiguous int32 tensor with B*H*SQ elements")
+        # Same footprint as the reference's workspace (peco/attention_cuda.py:112-113,128).
+        workspace = torch.empty(batch * heads * stride, dtype=torch.int32, device=q.device)
+        library = _native.library()
+        stream = _native.current_stream(q.device, q, k, v, dynamic_map, q_sizes, k_sizes, workspace, output, out_index)
+        error = library.peco_sparse_attention_ex(
+            _native.ptr(q), _native.ptr(k), _native.ptr(v), _native.ptr(dynamic_map), _native.ptr(q_sizes),
+            _native.ptr(k_sizes), _native.ptr(output), _native.ptr(out_index), _native.ptr(workspace),
+            workspace.numel(), batch * heads, sq, sk, dim, cq, ck, 0 if q.dtype == torch.float16 else 1, stream,
+        )
+        if error:
+            message = library.peco_attention_error_string(error).decode("utf-8", errors="replace")
+            raise RuntimeError(f"PECO HIP sparse attention launch failed: {message} ({error})")
+        return output

@@ -1,0 +1,198 @@
+"""PECO clustering kernels on gfx950 through the C-ABI (peco/clustering_cuda.py interface).
+
+The module name is kept from the reference so callers can switch imports unchanged.
+Clustering reads FP32/BF16/FP16 features and writes FP32 centres with int32
+labels/counts; token reordering copies FP16/BF16/FP32 feature bits unchanged.
+Every call is asynchronous on torch's current stream.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _native
+
+_DTYPES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+
+
+def build_cluster_library():
+    """Build the HIP library when missing or older than its sources; return its path."""
+    return _native.build_library()
+
+
+def _library():
+    return _native.library()
+
+
+def _raise_cluster_error(status):
+    """Raise for an immediate launch failure (peco/clustering_cuda.py:76-80)."""
+    if status:
+        message = _library().peco_cluster_error_message(status).decode("utf-8", errors="replace")
+        raise RuntimeError(f"HIP clustering failed: {message} (status {status})")
+
+
+def _retain_on_current_stream(device, *tensors):
+    return _native.current_stream(device, *tensors)
+
+
+def assign_tokens_to_centers(x, centers, labels, scratch, center_norms, chunk_size):
+    """Assign FP32 x [B,N,D] to centers [B,C,D], writing int32 labels [B,N].
+
+    ``center_norms`` [B,C] receives the centre norms. ``scratch`` and ``chunk_size``
+    are accepted for interface compatibility; the MFMA kernel needs no N-by-C scratch.
+    """
+    library = _library()
+    batch, tokens, dims = x.shape
+    clusters = centers.shape[1]
+    with torch.cuda.device(x.device):
+        status = library.peco_assign_tokens_to_centers(
+            _native.ptr(x), _native.ptr(centers), _native.ptr(labels), _native.ptr(scratch),
+            _native.ptr(center_norms), batch, tokens, dims, clusters, chunk_size,
+            _retain_on_current_stream(x.device, x, centers, labels, scratch, center_norms),
+        )
+    _raise_cluster_error(status)
+
+
+def recompute_cluster_centers(x, labels, previous, sums, counts, means):
+    """Write FP32 means [B,C,D] and int32 counts [B,C] for labels [B,N].
+
+    ``sums`` [B,C,D] receives the per-cluster sums; empty clusters keep ``previous``.
+    """
+    library = _library()
+    batch, tokens, dims = x.shape
+    with torch.cuda.device(x.device):
+        status = library.peco_recompute_cluster_centers(
+            _native.ptr(x), _native.ptr(labels), _native.ptr(previous), _native.ptr(sums),
+            _native.ptr(counts), _native.ptr(means), batch, tokens, dims, previous.shape[1],
+            _retain_on_current_stream(x.device, x, labels, previous, sums, counts, means),
+        )
+    _raise_cluster_error(status)
+
+
+def reorder_token_features(tensor, indices, inverse=False):
+    """Reorder features [B,H,N,D] using original token IDs [B*H,N].
+
+    Forward gathers original IDs into sorted order; inverse scatters sorted rows back.
+    """
+    library = _library()
+    tensor = tensor.contiguous()
+    indices = indices.to(dtype=torch.int32).contiguous()
+    batch, heads, tokens, dims = tensor.shape
+    result = torch.empty_like(tensor)
+    with torch.cuda.device(tensor.device):
+        status = library.peco_reorder_token_features(
+            _native.ptr(tensor), _native.ptr(indices), _native.ptr(result), batch * heads, tokens, dims,
+            tensor.element_size(), int(inverse), _retain_on_current_stream(tensor.device, tensor, indices, result),
+        )
+    _raise_cluster_error(status)
+    return result
+
+
+def cluster_sort(labels, clusters):
+    """Stable sort of int32 labels [B,N] with values in [0, clusters).
+
+    Returns (indices [B,N], counts [B,C], offsets [B,C+1]) where indices[b, j] is the
+    original token at sorted position j (== torch.argsort(labels, stable=True)).
+    """
+    library = _library()
+    labels = labels.to(torch.int32).contiguous()
+    batch, tokens = labels.shape
+    dev = labels.device
+    indices = torch.empty((batch, tokens), dtype=torch.int32, device=dev)
+    counts = torch.empty((batch, clusters), dtype=torch.int32, device=dev)
+    offsets = torch.empty((batch, clusters + 1), dtype=torch.int32, device=dev)
+    ws_bytes = library.peco_cluster_sort_workspace_size(batch, tokens, clusters)
+    ws = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        status = library.peco_cluster_sort(
+            _native.ptr(labels), batch, tokens, clusters, _native.ptr(indices), None, _native.ptr(counts),
+            _native.ptr(offsets), _native.ptr(ws), ws.numel(),
+            _retain_on_current_stream(dev, labels, indices, counts, offsets, ws),
+        )
+    _raise_cluster_error(status)
+    return indices, counts, offsets
+
+
+class KMeansProblem:
+    """One k-means problem for :func:`kmeans_fit`: x [B,N,D] (rows may have a batch stride)."""
+
+    def __init__(self, x, init_centers):
+        if x.ndim != 3 or x.stride(2) != 1 or x.stride(1) != x.shape[2]:
+            raise ValueError("x must be [B,N,D] with contiguous token rows")
+        self.x = x
+        self.init = init_centers.float().contiguous()
+        self.batch, self.tokens, self.dims = x.shape
+        self.clusters = self.init.shape[1]
+
+
+def kmeans_fit(problems, iterations):
+    """Fused Lloyd fit of one or two problems in shared launches.
+
+    Returns, per problem, (labels int32 [B,N], centers fp32 [B,K,D], counts int32 [B,K],
+    indices int32 [B,N], offsets int32 [B,K+1]); indices is the stable sort of labels.
+    """
+    library = _library()
+    if not 1 <= len(problems) <= 2:
+        raise ValueError("kmeans_fit takes one or two problems")
+    dims = problems[0].dims
+    dtype = problems[0].x.dtype
+    dev = problems[0].x.device
+    if any(p.dims != dims or p.x.dtype != dtype or p.x.device != dev for p in problems):
+        raise ValueError("kmeans_fit problems must share dims, dtype and device")
+    outs = []
+    ws_bytes = 0
+    for p in problems:
+        outs.append((
+            torch.empty((p.batch, p.tokens), dtype=torch.int32, device=dev),
+            torch.empty((p.batch, p.clusters, dims), dtype=torch.float32, device=dev),
+            torch.empty((p.batch, p.clusters), dtype=torch.int32, device=dev),
+            torch.empty((p.batch, p.tokens), dtype=torch.int32, device=dev),
+            torch.empty((p.batch, p.clusters + 1), dtype=torch.int32, device=dev),
+        ))
+        ws_bytes += library.peco_kmeans_workspace_size(p.batch, p.tokens, p.clusters, dims)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    strides = (ctypes.c_int64 * len(problems))(*[p.x.stride(0) for p in problems])
+    tensors = [p.x for p in problems] + [p.init for p in problems] + [t for o in outs for t in o] + [ws]
+    with torch.cuda.device(dev):
+        status = library.peco_kmeans_fit(
+            len(problems),
+            _native.ptr_array([p.x for p in problems]), ctypes.cast(strides, ctypes.c_void_p),
+            _native.ptr_array([p.init for p in problems]),
+            _native.ptr_array([o[1] for o in outs]), _native.ptr_array([o[0] for o in outs]),
+            _native.ptr_array([o[2] for o in outs]), _native.ptr_array([o[3] for o in outs]),
+            _native.ptr_array([o[4] for o in outs]),
+            _native.int_array([p.batch for p in problems]), _native.int_array([p.tokens for p in problems]),
+            _native.int_array([p.clusters for p in problems]), dims, _DTYPES[dtype], int(iterations),
+            _native.ptr(ws), ws_bytes, _retain_on_current_stream(dev, *tensors),
+        )
+    _raise_cluster_error(status)
+    return outs
+
+
+def pack_clustered(tensors, indices, labels, centroids, bits, video):
+    """Gather up to three [B,H,S,D] tensors into cluster order in one launch.
+
+    Rows [0, video) of tensor i are taken in the order of indices[i] [B*H, video]; when
+    bits[i] is 4 or 8 they are Base-Offset fake-quantized against (labels[i], centroids[i])
+    on the way. Rows [video, S) (text) are copied unchanged. Returns new tensors.
+    """
+    library = _library()
+    ref = tensors[0]
+    b, h, s, d = ref.shape
+    outs = [torch.empty_like(t) for t in tensors]
+    n = len(tensors)
+    clusters = [0 if c is None else c.shape[1] for c in centroids]
+    with torch.cuda.device(ref.device):
+        status = library.peco_pack_clustered(
+            _native.ptr_array(tensors), _native.ptr_array(outs), _native.ptr_array(indices),
+            _native.ptr_array(labels), _native.ptr_array(centroids), _native.int_array(clusters),
+            _native.int_array(bits), n, b * h, s, video, d, _DTYPES[ref.dtype],
+            _retain_on_current_stream(ref.device, *tensors, *outs, *[t for t in indices + labels + centroids]),
+        )
+    _raise_cluster_error(status)
+    return outs
+
+
+if __name__ == "__main__":
+    print(build_cluster_library())

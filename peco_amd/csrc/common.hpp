@@ -1,0 +1,92 @@
+// Shared device helpers for the PECO gfx950 kernels.
+//
+// All kernels are written for CDNA4 (gfx950): 64-lane wavefronts, MFMA matrix cores,
+// 160 KB LDS per CU. Exact fp32 arithmetic matters for the k-means labels and the
+// Base-Offset codes, so every translation unit is compiled with -ffp-contract=off and
+// correctly rounded fp32 division; fused multiply-adds are written explicitly.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define PECO_API extern "C" __attribute__((visibility("default")))
+
+namespace peco {
+
+constexpr int kWave = 64;
+
+// PECO-specific status codes live above the hipError_t range.
+enum Status : int {
+    kOk = 0,
+    kInvalidValue = 1,          // == hipErrorInvalidValue
+    kWorkspaceTooSmall = 20001,
+    kUnsupportedShape = 20002,
+    kUnsupportedDtype = 20003,
+};
+
+enum DType : int { kF16 = 0, kBF16 = 1, kF32 = 2 };
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+    return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// fp32 -> bf16 with round-to-nearest-even (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return static_cast<uint16_t>((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, b));
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+template <int DT> __device__ __forceinline__ float load_elem(const void* p, int64_t i);
+template <> __device__ __forceinline__ float load_elem<kBF16>(const void* p, int64_t i) {
+    return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+template <> __device__ __forceinline__ float load_elem<kF16>(const void* p, int64_t i) {
+    return f16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+template <> __device__ __forceinline__ float load_elem<kF32>(const void* p, int64_t i) {
+    return static_cast<const float*>(p)[i];
+}
+
+// Unpack 16-bit payloads (bf16 or fp16, chosen at compile time) to fp32.
+template <int DT> __device__ __forceinline__ float half_to_f32(uint16_t b) {
+    if constexpr (DT == kBF16) return bf16_bits_to_f32(b);
+    else return f16_bits_to_f32(b);
+}
+template <int DT> __device__ __forceinline__ uint16_t f32_to_half(float f) {
+    if constexpr (DT == kBF16) return f32_to_bf16_bits(f);
+    else return f32_to_f16_bits(f);
+}
+
+// Order-preserving map of fp32 onto uint32 (for packed (value, index) min keys).
+__device__ __forceinline__ uint32_t orderable(float f) {
+    uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+template <typename T> __device__ __forceinline__ T wave_shfl_xor(T v, int mask) {
+    return __shfl_xor(v, mask, kWave);
+}
+
+__host__ __device__ __forceinline__ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace peco

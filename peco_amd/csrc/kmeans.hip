@@ -1,0 +1,639 @@
+// Stage 1: batched Lloyd k-means over Q and K per (batch, head), for gfx950.
+//
+// Reference semantics (peco/clustering.py:45-89, CPU branch; tie rule kmeans.cu:43,55-56):
+//   label[t] = argmin_j ( -2 x_t.c_j + |c_j|^2 ), lowest j on ties
+//   mean[j]  = (sum of member rows) / count, or the previous centre when empty.
+// The fp32 order is fixed so results are reproducible bit for bit:
+//   n_j   = sum_d fl(c_jd^2), d ascending                      (centre norm)
+//   D_tj  = fma(-2, dot_tj, n_j), dot_tj = fma chain, d ascending
+//   sum_j = fp32 adds of member rows in original token order   (== torch scatter_add_)
+//
+// Assignment never evaluates D_tj for every pair. A bf16 MFMA screen computes
+//   S_tj = x_t . (c_hi + c_lo)*(-2)   with c_hi = bf16(c), c_lo = bf16(c - c_hi)
+// (x itself is split the same way when it is not bf16), whose error against the exact
+// dot product is bounded a priori (|c - c_hi - c_lo| <= 2^-16 |c|, products exact in fp32,
+// fp32 accumulation error <= gamma_n). With screened minimum m1 (at id1), second minimum m2
+// and the bound E on |screened - canonical| for any centre, m2 - m1 > 2E proves that id1 is
+// the canonical argmin. Tokens that fail the test are re-evaluated in-kernel with the
+// canonical fp32 formula over all centres. Labels are therefore identical to the canonical
+// fixed-order fp32 definition, not approximately equal.
+//
+// Per iteration: assign (+ per-tile label histogram via global atomics) -> sort scan ->
+// sort place (stable counting sort, also yields the final permutation for stage 3) ->
+// update (sequential per-cluster sums in token order; also prepares the next iteration's
+// split-bf16 centres and canonical norms). Q and K fits share every launch.
+#include "common.hpp"
+#include "sort.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <vector>
+
+namespace peco {
+
+struct KmProblem {
+    const void* x;          // [batch, tokens, D] rows (dtype of the fit); batch stride x_stride
+    int64_t x_stride;       // elements between consecutive batch entries of x (>= tokens * D)
+    const float* centers_in;  // [batch, K, D] initial centres (read only)
+    float* centers_out;     // [batch, K, D] final centres
+    float* centers_tmp;     // [batch, K, D] ping-pong buffer
+    int32_t* labels;        // [batch, tokens]
+    int32_t* counts;        // [batch, K]
+    int32_t* indices;       // [batch, tokens] stable sort of the final labels
+    int32_t* offsets;       // [batch, K + 1]
+    uint16_t* prep_hi;      // [batch, K, D] bf16(-2 c)
+    uint16_t* prep_lo;      // [batch, K, D] bf16(-2 c - hi)
+    float* norms;           // [batch, K] canonical norms of the current centres
+    int32_t* tile_hist;     // [batch, sort tiles, K]
+    float* sums;            // nullable [batch, K, D]: per-cluster sums of the last update
+    int batch, tokens, clusters;
+    int assign_begin;       // first linear assign block (batch * ceil(tokens/128) blocks)
+    int update_begin;       // first linear update block (batch * K blocks)
+    int sort_tiles;
+};
+
+constexpr int kMaxKm = 2;
+constexpr int kAssignTile = 128;  // tokens per assign workgroup (4 waves x 32 tokens)
+
+struct KmArgs {
+    KmProblem p[kMaxKm];
+    int num;
+    int total_assign_blocks;
+    int total_update_blocks;
+    float kappa;  // bound coefficient: |screened - canonical| <= kappa*|x||c| + rounding terms
+};
+
+struct KmIter {
+    const float* src[kMaxKm];  // centres used by this iteration
+    float* dst[kMaxKm];        // means written by this iteration
+};
+
+namespace {
+
+__device__ __forceinline__ int km_problem(const KmArgs& a, int block, bool assign) {
+    int p = 0;
+    if (assign) {
+        while (p + 1 < a.num && block >= a.p[p + 1].assign_begin) ++p;
+    } else {
+        while (p + 1 < a.num && block >= a.p[p + 1].update_begin) ++p;
+    }
+    return p;
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u16x8 u) { return __builtin_bit_cast(bf16x8, u); }
+
+// Canonical norm and split-bf16 preparation of one centre row held in LDS.
+__device__ __forceinline__ float canonical_norm_lds(const float* row, int D) {
+    float s = 0.0f;
+    for (int d = 0; d < D; ++d) {
+        const float sq = row[d] * row[d];
+        s = s + sq;
+    }
+    return s;
+}
+
+__device__ __forceinline__ void split_neg2(float c, uint16_t& hi, uint16_t& lo) {
+    const float v = -2.0f * c;
+    hi = f32_to_bf16_bits(v);
+    lo = f32_to_bf16_bits(v - bf16_bits_to_f32(hi));
+}
+
+// Initial preparation: norms + split of the initial centres; clears the tile histograms.
+template <int D>
+__global__ __launch_bounds__(64) void km_prep_kernel(KmArgs a, KmIter it) {
+    __shared__ float row[D];
+    int p = 0;
+    int block = blockIdx.x;
+    while (p + 1 < a.num && block >= a.p[p + 1].update_begin) ++p;
+    const KmProblem& P = a.p[p];
+    const int local = block - P.update_begin;  // b * K + j
+    const float* c = it.src[p] + static_cast<int64_t>(local) * D;
+    for (int d = threadIdx.x; d < D; d += kWave) {
+        const float v = c[d];
+        row[d] = v;
+        uint16_t hi, lo;
+        split_neg2(v, hi, lo);
+        P.prep_hi[static_cast<int64_t>(local) * D + d] = hi;
+        P.prep_lo[static_cast<int64_t>(local) * D + d] = lo;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) P.norms[local] = canonical_norm_lds(row, D);
+    // Clear this problem's tile histograms (strided over the problem's blocks).
+    const int64_t hist = static_cast<int64_t>(P.batch) * P.sort_tiles * P.clusters;
+    const int64_t nblocks = static_cast<int64_t>(P.batch) * P.clusters;
+    for (int64_t i = static_cast<int64_t>(local) * kWave + threadIdx.x; i < hist; i += nblocks * kWave)
+        P.tile_hist[i] = 0;
+}
+
+// x operand (B of the MFMA): 8 consecutive channels of one token as bf16 (hi, and lo when split).
+template <int DT>
+__device__ __forceinline__ void load_x8(const void* x, int64_t e, bool valid, u16x8& hi, u16x8& lo, float& sq) {
+    if (!valid) {
+        hi = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        lo = hi;
+        return;
+    }
+    if constexpr (DT == kBF16) {
+        hi = *reinterpret_cast<const u16x8*>(static_cast<const uint16_t*>(x) + e);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float f = bf16_bits_to_f32(hi[i]);
+            sq = fmaf(f, f, sq);
+        }
+    } else {
+        float f[8];
+        if constexpr (DT == kF32) {
+            const f32x4 a = reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + e)[0];
+            const f32x4 b = reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + e)[1];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) { f[i] = a[i]; f[4 + i] = b[i]; }
+        } else {
+            const u16x8 u = *reinterpret_cast<const u16x8*>(static_cast<const uint16_t*>(x) + e);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) f[i] = f16_bits_to_f32(u[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint16_t h = f32_to_bf16_bits(f[i]);
+            hi[i] = h;
+            lo[i] = f32_to_bf16_bits(f[i] - bf16_bits_to_f32(h));
+            sq = fmaf(f[i], f[i], sq);
+        }
+    }
+}
+
+// Assign: one workgroup = 128 tokens of one (problem, batch); wave w owns tokens
+// [32w, 32w+32). MFMA 32x32x16: A = centres (32 rows x 16 channels), B = tokens
+// (16 channels x 32 tokens); lane l holds token l%32 and centres 8*(i/4)+4*(l/32)+i%4.
+template <int DT, int D>
+__global__ __launch_bounds__(256) void km_assign_kernel(KmArgs a, KmIter it) {
+    constexpr int S = D / 16;                 // MFMA k-steps over channels
+    constexpr bool kSplitX = DT != kBF16;
+    __shared__ float red[4];
+    const int p = km_problem(a, blockIdx.x, true);
+    const KmProblem& P = a.p[p];
+    const int local = blockIdx.x - P.assign_begin;
+    const int tiles_per_batch = static_cast<int>(ceil_div(P.tokens, kAssignTile));
+    const int b = local / tiles_per_batch;
+    const int tile = local % tiles_per_batch;
+    const int K = P.clusters;
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    const int h = lane / 32;
+    const int t = tile * kAssignTile + wave * 32 + (lane % 32);
+    const bool valid = t < P.tokens;
+    const int64_t row = static_cast<int64_t>(b) * P.tokens + t;
+    const int64_t xrow = static_cast<int64_t>(b) * P.x_stride + static_cast<int64_t>(t) * D;
+    const float* norms = P.norms + static_cast<int64_t>(b) * K;
+
+    // Largest centre norm of this batch entry (for the error bound).
+    float nmax = 0.0f;
+    for (int j = threadIdx.x; j < K; j += blockDim.x) nmax = fmaxf(nmax, norms[j]);
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) nmax = fmaxf(nmax, __shfl_xor(nmax, m, kWave));
+    if (lane == 0) red[wave] = nmax;
+    __syncthreads();
+    nmax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+
+    u16x8 xh[S], xl[S];
+    float sq = 0.0f;
+#pragma unroll
+    for (int s = 0; s < S; ++s) load_x8<DT>(P.x, xrow + 16 * s + 8 * h, valid, xh[s], xl[s], sq);
+    sq += __shfl_xor(sq, 32, kWave);
+
+    float m1 = INFINITY, m2 = INFINITY;
+    int id1 = 0;
+    const uint16_t* hi_base = P.prep_hi + static_cast<int64_t>(b) * K * D;
+    const uint16_t* lo_base = P.prep_lo + static_cast<int64_t>(b) * K * D;
+    for (int cb = 0; cb < K; cb += 32) {
+        const int crow = cb + (lane % 32);
+        const bool cvalid = crow < K;
+        f32x16 acc = {};
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            u16x8 ah = u16x8{0, 0, 0, 0, 0, 0, 0, 0}, al = ah;
+            if (cvalid) {
+                ah = *reinterpret_cast<const u16x8*>(hi_base + static_cast<int64_t>(crow) * D + 16 * s + 8 * h);
+                al = *reinterpret_cast<const u16x8*>(lo_base + static_cast<int64_t>(crow) * D + 16 * s + 8 * h);
+            }
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(ah), as_bf16x8(xh[s]), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(al), as_bf16x8(xh[s]), acc, 0, 0, 0);
+            if constexpr (kSplitX)
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(ah), as_bf16x8(xl[s]), acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int j = cb + 8 * g + 4 * h + r;
+                const float v = j < K ? acc[4 * g + r] + norms[j] : INFINITY;
+                const float nm2 = fminf(m2, fmaxf(m1, v));
+                id1 = v < m1 ? j : id1;
+                m1 = fminf(m1, v);
+                m2 = nm2;
+            }
+        }
+    }
+    // Merge the two lane halves that hold the same token.
+    {
+        const float pm1 = __shfl_xor(m1, 32, kWave);
+        const float pm2 = __shfl_xor(m2, 32, kWave);
+        const int pid = __shfl_xor(id1, 32, kWave);
+        const float nm2 = fminf(fminf(m2, pm2), fmaxf(m1, pm1));
+        if (pm1 < m1 || (pm1 == m1 && pid < id1)) {
+            m1 = pm1;
+            id1 = pid;
+        }
+        m2 = nm2;
+    }
+    // Certified decision: gap > 2E proves id1 is the canonical argmin.
+    const float xnorm = sqrtf(sq) * 1.001f;
+    const float cmax = sqrtf(nmax) * 1.001f;
+    const float thr = 1.05f * (2.0f * a.kappa * xnorm * cmax) + 4.0f * 5.9604645e-8f * (fabsf(m1) + fabsf(m2)) + 1e-30f;
+    const bool sure = (m2 - m1) > thr;
+    int label = id1;
+    const bool flagged = valid && !sure;
+
+    // Canonical re-evaluation of flagged tokens, one token at a time per wave.
+    uint64_t pending = __ballot(flagged && h == 0);
+    const float* cent = it.src[p] + static_cast<int64_t>(b) * K * D;
+    while (pending) {
+        const int src_lane = __builtin_ctzll(pending);
+        pending &= pending - 1;
+        const int tok = tile * kAssignTile + wave * 32 + src_lane;
+        const int64_t trow = static_cast<int64_t>(b) * P.x_stride + static_cast<int64_t>(tok) * D;
+        uint64_t best = ~0ull;
+        for (int j0 = 0; j0 < K; j0 += kWave) {
+            const int j = j0 + lane;
+            if (j < K) {
+                const float* c = cent + static_cast<int64_t>(j) * D;
+                float dot = 0.0f;
+                for (int d = 0; d < D; d += 4) {
+                    const f32x4 cv = *reinterpret_cast<const f32x4*>(c + d);
+                    dot = fmaf(load_elem<DT>(P.x, trow + d + 0), cv[0], dot);
+                    dot = fmaf(load_elem<DT>(P.x, trow + d + 1), cv[1], dot);
+                    dot = fmaf(load_elem<DT>(P.x, trow + d + 2), cv[2], dot);
+                    dot = fmaf(load_elem<DT>(P.x, trow + d + 3), cv[3], dot);
+                }
+                const float dist = fmaf(-2.0f, dot, norms[j]);
+                const uint64_t key = (static_cast<uint64_t>(orderable(dist)) << 32) | static_cast<uint32_t>(j);
+                best = key < best ? key : best;
+            }
+        }
+#pragma unroll
+        for (int m = 1; m < kWave; m <<= 1) {
+            const uint64_t o = __shfl_xor(best, m, kWave);
+            best = o < best ? o : best;
+        }
+        if ((lane % 32) == src_lane) label = static_cast<int>(best & 0xffffffffu);
+    }
+    if (valid && h == 0) {
+        P.labels[row] = label;
+        atomicAdd(P.tile_hist + (static_cast<int64_t>(b) * P.sort_tiles + t / kSortTile) * K + label, 1);
+    }
+}
+
+// Update: one wavefront per (problem, batch, cluster). Sums member rows in original token
+// order (the sorted member list is stable), divides by the count, and prepares the next
+// iteration's split centres and canonical norm.
+template <int DT, int D>
+__global__ __launch_bounds__(64) void km_update_kernel(KmArgs a, KmIter it) {
+    constexpr int PER = D / kWave;  // channels per lane (1 or 2)
+    __shared__ float row[D];
+    const int p = km_problem(a, blockIdx.x, false);
+    const KmProblem& P = a.p[p];
+    const int local = blockIdx.x - P.update_begin;  // b * K + j
+    const int K = P.clusters;
+    const int b = local / K;
+    const int j = local % K;
+    const int lane = threadIdx.x;
+    const int32_t* off = P.offsets + static_cast<int64_t>(b) * (K + 1);
+    const int begin = off[j], end = off[j + 1];
+    const int32_t* idx = P.indices + static_cast<int64_t>(b) * P.tokens;
+    const int64_t xbase = static_cast<int64_t>(b) * P.x_stride + lane * PER;
+    float s[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) s[i] = 0.0f;
+    int m = begin;
+    for (; m + 4 <= end; m += 4) {
+        float v[4][PER];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t e = xbase + static_cast<int64_t>(idx[m + u]) * D;
+#pragma unroll
+            for (int i = 0; i < PER; ++i) v[u][i] = load_elem<DT>(P.x, e + i);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int i = 0; i < PER; ++i) s[i] = s[i] + v[u][i];
+    }
+    for (; m < end; ++m) {
+        const int64_t e = xbase + static_cast<int64_t>(idx[m]) * D;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) s[i] = s[i] + load_elem<DT>(P.x, e + i);
+    }
+    const int count = end - begin;
+    const int64_t cbase = static_cast<int64_t>(local) * D + lane * PER;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const float mean = count > 0 ? s[i] / static_cast<float>(count) : it.src[p][cbase + i];
+        it.dst[p][cbase + i] = mean;
+        if (P.sums) P.sums[cbase + i] = s[i];
+        row[lane * PER + i] = mean;
+        uint16_t hi, lo;
+        split_neg2(mean, hi, lo);
+        P.prep_hi[cbase + i] = hi;
+        P.prep_lo[cbase + i] = lo;
+    }
+    __syncthreads();
+    if (lane == 0) P.norms[local] = canonical_norm_lds(row, D);
+}
+
+template <int DT, int D>
+hipError_t run_fit(KmArgs& a, const KmIter* iters, int iterations, const SortArgs& sa, hipStream_t s) {
+    hipLaunchKernelGGL((km_prep_kernel<D>), dim3(a.total_update_blocks), dim3(64), 0, s, a, iters[0]);
+    for (int i = 0; i < iterations; ++i) {
+        hipLaunchKernelGGL((km_assign_kernel<DT, D>), dim3(a.total_assign_blocks), dim3(256), 0, s, a, iters[i]);
+        hipError_t e = launch_cluster_sort(sa, s, false);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL((km_update_kernel<DT, D>), dim3(a.total_update_blocks), dim3(64), 0, s, a, iters[i]);
+    }
+    return hipGetLastError();
+}
+
+// gamma_n = n u / (1 - n u), u = 2^-24.
+double gamma_n(double n) {
+    const double u = std::ldexp(1.0, -24);
+    return n * u / (1.0 - n * u);
+}
+
+}  // namespace
+
+// Coefficient of |x||c| in the bound on |screened - canonical| distance.
+float km_kappa(int dtype, int dims) {
+    const double split = std::ldexp(1.0, -16);
+    double screen;
+    if (dtype == kBF16) screen = split + gamma_n(2.0 * dims + 1) * (1.0 + std::ldexp(1.0, -7));
+    else screen = 3.0 * split + gamma_n(3.0 * dims + 1) * (1.0 + std::ldexp(1.0, -6));
+    const double canonical = gamma_n(dims);
+    return static_cast<float>(2.0 * (screen + canonical));
+}
+
+struct KmFitDesc {
+    const void* x;
+    int64_t x_stride;
+    const float* centers_in;
+    float* centers_out;
+    int32_t* labels;
+    int32_t* counts;
+    int32_t* indices;
+    int32_t* offsets;
+    int batch, tokens, clusters;
+};
+
+// Workspace (bytes) for one problem.
+size_t km_workspace_bytes(int batch, int tokens, int clusters, int dims) {
+    const size_t bkd = static_cast<size_t>(batch) * clusters * dims;
+    size_t bytes = 0;
+    auto add = [&](size_t n) { bytes += (n + 63) / 64 * 64; };
+    add(bkd * sizeof(float));                       // ping-pong centres
+    add(bkd * sizeof(uint16_t));                    // prep hi
+    add(bkd * sizeof(uint16_t));                    // prep lo
+    add(static_cast<size_t>(batch) * clusters * sizeof(float));  // norms
+    add(sort_workspace_ints(batch, tokens, clusters) * sizeof(int32_t));
+    return bytes;
+}
+
+hipError_t km_fit(const KmFitDesc* descs, int num, int dims, int dtype, int iterations, void* workspace,
+                  float* sums, hipStream_t stream) {
+    KmArgs a{};
+    SortArgs sa{};
+    a.num = num;
+    sa.num = num;
+    sa.zero_hist = 1;
+    char* ws = static_cast<char*>(workspace);
+    auto take = [&](size_t n) {
+        char* p = ws;
+        ws += (n + 63) / 64 * 64;
+        return p;
+    };
+    int ab = 0, ub = 0;
+    for (int i = 0; i < num; ++i) {
+        const KmFitDesc& d = descs[i];
+        KmProblem& P = a.p[i];
+        const size_t bkd = static_cast<size_t>(d.batch) * d.clusters * dims;
+        P.x = d.x;
+        P.x_stride = d.x_stride > 0 ? d.x_stride : static_cast<int64_t>(d.tokens) * dims;
+        P.centers_in = d.centers_in;
+        P.centers_out = d.centers_out;
+        P.centers_tmp = reinterpret_cast<float*>(take(bkd * sizeof(float)));
+        P.prep_hi = reinterpret_cast<uint16_t*>(take(bkd * sizeof(uint16_t)));
+        P.prep_lo = reinterpret_cast<uint16_t*>(take(bkd * sizeof(uint16_t)));
+        P.norms = reinterpret_cast<float*>(take(static_cast<size_t>(d.batch) * d.clusters * sizeof(float)));
+        P.tile_hist = reinterpret_cast<int32_t*>(take(sort_workspace_ints(d.batch, d.tokens, d.clusters) * sizeof(int32_t)));
+        P.labels = d.labels;
+        P.counts = d.counts;
+        P.indices = d.indices;
+        P.offsets = d.offsets;
+        P.sums = (num == 1) ? sums : nullptr;
+        P.batch = d.batch;
+        P.tokens = d.tokens;
+        P.clusters = d.clusters;
+        P.sort_tiles = sort_tiles(d.tokens);
+        P.assign_begin = ab;
+        P.update_begin = ub;
+        ab += d.batch * static_cast<int>(ceil_div(d.tokens, kAssignTile));
+        ub += d.batch * d.clusters;
+        SortProblem& q = sa.p[i];
+        q.labels = d.labels;
+        q.indices = d.indices;
+        q.ranks = nullptr;
+        q.counts = d.counts;
+        q.offsets = d.offsets;
+        q.tile_hist = P.tile_hist;
+        q.batch = d.batch;
+        q.tokens = d.tokens;
+        q.clusters = d.clusters;
+    }
+    a.total_assign_blocks = ab;
+    a.total_update_blocks = ub;
+    a.kappa = km_kappa(dtype, dims);
+    sort_args_finalize(sa);
+    std::vector<KmIter> iters(std::max(iterations, 1));
+    for (int i = 0; i < iterations; ++i) {
+        for (int q = 0; q < num; ++q) {
+            float* dst = ((iterations - 1 - i) % 2 == 0) ? a.p[q].centers_out : a.p[q].centers_tmp;
+            iters[i].dst[q] = dst;
+            iters[i].src[q] = i == 0 ? a.p[q].centers_in : iters[i - 1].dst[q];
+        }
+    }
+#define PECO_FIT(DT_, D_) return run_fit<DT_, D_>(a, iters.data(), iterations, sa, stream)
+    if (dims == 128) {
+        if (dtype == kBF16) PECO_FIT(kBF16, 128);
+        if (dtype == kF16) PECO_FIT(kF16, 128);
+        if (dtype == kF32) PECO_FIT(kF32, 128);
+    } else if (dims == 64) {
+        if (dtype == kBF16) PECO_FIT(kBF16, 64);
+        if (dtype == kF16) PECO_FIT(kF16, 64);
+        if (dtype == kF32) PECO_FIT(kF32, 64);
+    }
+#undef PECO_FIT
+    return static_cast<hipError_t>(kUnsupportedShape);
+}
+
+}  // namespace peco
+
+using namespace peco;
+
+namespace {
+bool valid_fit(const KmFitDesc& d) {
+    return d.x && d.centers_in && d.centers_out && d.labels && d.counts && d.indices && d.offsets && d.batch >= 1 &&
+           d.tokens >= 1 && d.clusters >= 1 && d.clusters <= d.tokens && d.clusters <= kMaxSortClusters;
+}
+}  // namespace
+
+PECO_API size_t peco_kmeans_workspace_size(int batch, int tokens, int clusters, int dims) {
+    if (batch < 1 || tokens < 1 || clusters < 1 || dims < 1) return 0;
+    return km_workspace_bytes(batch, tokens, clusters, dims);
+}
+
+// Fused fit of one or two independent problems (e.g. Q with KQ centres and K with KK
+// centres) sharing every launch. Problem i is described by the i-th element of each array.
+PECO_API int peco_kmeans_fit(int num_problems, const void* const* x, const int64_t* x_batch_stride,
+                             const float* const* centers_in,
+                             float* const* centers_out, int32_t* const* labels, int32_t* const* counts,
+                             int32_t* const* sorted_indices, int32_t* const* offsets, const int* batch,
+                             const int* tokens, const int* clusters, int dims, int dtype, int iterations,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+    if (num_problems < 1 || num_problems > kMaxKm || iterations < 1 || (dims != 64 && dims != 128) ||
+        (dtype != kBF16 && dtype != kF16 && dtype != kF32) || !workspace)
+        return kInvalidValue;
+    KmFitDesc d[kMaxKm];
+    size_t need = 0;
+    for (int i = 0; i < num_problems; ++i) {
+        const int64_t stride = x_batch_stride ? x_batch_stride[i] : 0;
+        d[i] = KmFitDesc{x[i], stride, centers_in[i], centers_out[i], labels[i], counts[i], sorted_indices[i],
+                         offsets[i], batch[i], tokens[i], clusters[i]};
+        if (!valid_fit(d[i]) || (stride != 0 && stride < static_cast<int64_t>(tokens[i]) * dims)) return kInvalidValue;
+        need += km_workspace_bytes(batch[i], tokens[i], clusters[i], dims);
+    }
+    if (workspace_bytes < need) return kWorkspaceTooSmall;
+    return km_fit(d, num_problems, dims, dtype, iterations, workspace, nullptr, static_cast<hipStream_t>(stream));
+}
+
+// Reference ABI (peco/kernels/kmeans.cu:139): one assignment of fp32 x [B,N,D] to centres
+// [B,C,D]. scratch/chunk_size are accepted for ABI compatibility and unused; center_norms
+// receives the canonical norms. Internal buffers come from the stream-ordered allocator.
+PECO_API int peco_assign_tokens_to_centers(const float* x, const float* centers, int32_t* labels, float* scratch,
+                                           float* center_norms, int batch, int tokens, int dims, int clusters,
+                                           int chunk_size, void* stream) {
+    (void)scratch;
+    (void)chunk_size;
+    if (!x || !centers || !labels || batch < 1 || tokens < 1 || clusters < 1 || (dims != 64 && dims != 128))
+        return kInvalidValue;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    KmArgs a{};
+    a.num = 1;
+    KmProblem& P = a.p[0];
+    const size_t bkd = static_cast<size_t>(batch) * clusters * dims;
+    const size_t hist = sort_workspace_ints(batch, tokens, clusters);
+    void* buf = nullptr;
+    const size_t bytes = bkd * 4 + (center_norms ? 0 : static_cast<size_t>(batch) * clusters * 4) + hist * 4 + 256;
+    hipError_t e = hipMallocAsync(&buf, bytes, s);
+    if (e != hipSuccess) return e;
+    char* w = static_cast<char*>(buf);
+    P.x = x;
+    P.x_stride = static_cast<int64_t>(tokens) * dims;
+    P.prep_hi = reinterpret_cast<uint16_t*>(w);
+    P.prep_lo = P.prep_hi + bkd;
+    w += bkd * 4;
+    if (center_norms) P.norms = center_norms;
+    else { P.norms = reinterpret_cast<float*>(w); w += static_cast<size_t>(batch) * clusters * 4; }
+    P.tile_hist = reinterpret_cast<int32_t*>(w);
+    P.labels = labels;
+    P.batch = batch;
+    P.tokens = tokens;
+    P.clusters = clusters;
+    P.sort_tiles = sort_tiles(tokens);
+    a.total_assign_blocks = batch * static_cast<int>(ceil_div(tokens, kAssignTile));
+    a.total_update_blocks = batch * clusters;
+    a.kappa = km_kappa(kF32, dims);
+    KmIter it{};
+    it.src[0] = centers;
+    if (dims == 128) {
+        hipLaunchKernelGGL((km_prep_kernel<128>), dim3(a.total_update_blocks), dim3(64), 0, s, a, it);
+        hipLaunchKernelGGL((km_assign_kernel<kF32, 128>), dim3(a.total_assign_blocks), dim3(256), 0, s, a, it);
+    } else {
+        hipLaunchKernelGGL((km_prep_kernel<64>), dim3(a.total_update_blocks), dim3(64), 0, s, a, it);
+        hipLaunchKernelGGL((km_assign_kernel<kF32, 64>), dim3(a.total_assign_blocks), dim3(256), 0, s, a, it);
+    }
+    e = hipGetLastError();
+    hipError_t f = hipFreeAsync(buf, s);
+    return e != hipSuccess ? e : f;
+}
+
+// Reference ABI (peco/kernels/kmeans.cu:179): means/counts of fp32 x [B,N,D] for labels
+// [B,N]; sums receives the per-cluster sums; empty clusters keep `previous`.
+PECO_API int peco_recompute_cluster_centers(const float* x, const int32_t* labels, const float* previous, float* sums,
+                                            int32_t* counts, float* means, int batch, int tokens, int dims,
+                                            int clusters, void* stream) {
+    if (!x || !labels || !previous || !counts || !means || batch < 1 || tokens < 1 || clusters < 1 ||
+        clusters > kMaxSortClusters || (dims != 64 && dims != 128))
+        return kInvalidValue;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const size_t bkd = static_cast<size_t>(batch) * clusters * dims;
+    const size_t hist = sort_workspace_ints(batch, tokens, clusters);
+    const size_t idx = static_cast<size_t>(batch) * tokens;
+    const size_t off = static_cast<size_t>(batch) * (clusters + 1);
+    const size_t nrm = static_cast<size_t>(batch) * clusters;
+    void* buf = nullptr;
+    hipError_t e = hipMallocAsync(&buf, (bkd * 2 + hist + idx + off + nrm) * 4 + 256, s);
+    if (e != hipSuccess) return e;
+    char* w = static_cast<char*>(buf);
+    SortArgs sa{};
+    sa.num = 1;
+    SortProblem& q = sa.p[0];
+    q.labels = labels;
+    q.indices = reinterpret_cast<int32_t*>(w);
+    w += idx * 4;
+    q.offsets = reinterpret_cast<int32_t*>(w);
+    w += off * 4;
+    q.tile_hist = reinterpret_cast<int32_t*>(w);
+    w += hist * 4;
+    q.counts = counts;
+    q.ranks = nullptr;
+    q.batch = batch;
+    q.tokens = tokens;
+    q.clusters = clusters;
+    sort_args_finalize(sa);
+    e = launch_cluster_sort(sa, s, true);
+    if (e == hipSuccess) {
+        KmArgs a{};
+        a.num = 1;
+        KmProblem& P = a.p[0];
+        P.x = x;
+        P.x_stride = static_cast<int64_t>(tokens) * dims;
+        P.indices = q.indices;
+        P.offsets = q.offsets;
+        P.prep_hi = reinterpret_cast<uint16_t*>(w);
+        P.prep_lo = P.prep_hi + bkd;
+        w += bkd * 4;
+        P.norms = reinterpret_cast<float*>(w);
+        P.sums = sums;
+        P.batch = batch;
+        P.tokens = tokens;
+        P.clusters = clusters;
+        a.total_update_blocks = batch * clusters;
+        KmIter it{};
+        it.src[0] = previous;
+        it.dst[0] = means;
+        if (dims == 128)
+            hipLaunchKernelGGL((km_update_kernel<kF32, 128>), dim3(a.total_update_blocks), dim3(64), 0, s, a, it);
+        else
+            hipLaunchKernelGGL((km_update_kernel<kF32, 64>), dim3(a.total_update_blocks), dim3(64), 0, s, a, it);
+        e = hipGetLastError();
+    }
+    hipError_t f = hipFreeAsync(buf, s);
+    return e != hipSuccess ? e : f;
+}

@@ -1,0 +1,318 @@
+// Stage 2: Base-Offset PE centroid-residual quantizer (peco/quantization.py:97-150),
+// plus the fused "pack" kernel that applies it while gathering Q/K/V into cluster order
+// and appending the unsorted text rows (peco/processor.py:141-149).
+//
+// Per token, over all D channels, in this fp32 order (one rounding per line):
+//   r = x - C[label]; low = min r; high = max r
+//   scale = (high - low) / (2^bits - 1), or 1 when not positive
+//   code  = clamp(rint((r - low) / scale), 0, 2^bits - 1)      (rint = half-to-even)
+//   xhat  = C[label] + (low + scale * code), cast to the input dtype (RNE)
+// The translation unit is built with -ffp-contract=off and correctly rounded division,
+// so every line above is one IEEE operation, as in the torch reference.
+//
+// Layout: a token row of D elements is handled by G = D/8 lanes (8 elements per lane,
+// 16-byte loads for 16-bit inputs), so one wavefront covers 64/G rows and min/max are
+// reduced with log2(G) xor-shuffles inside the lane group. HBM-bound streaming kernel.
+#include "common.hpp"
+
+#include <algorithm>
+
+namespace peco {
+namespace {
+
+template <int DT> struct Row8 {
+    // Loads 8 consecutive elements (starting at element offset e) as fp32.
+    __device__ __forceinline__ static void load(const void* base, int64_t e, float (&v)[8]) {
+        if constexpr (DT == kF32) {
+            const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(base) + e);
+            const f32x4 a = p[0], b = p[1];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) { v[i] = a[i]; v[4 + i] = b[i]; }
+        } else {
+            const u16x8 u = *reinterpret_cast<const u16x8*>(static_cast<const uint16_t*>(base) + e);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = half_to_f32<DT>(u[i]);
+        }
+    }
+    __device__ __forceinline__ static void store(void* base, int64_t e, const float (&v)[8]) {
+        if constexpr (DT == kF32) {
+            f32x4* p = reinterpret_cast<f32x4*>(static_cast<float*>(base) + e);
+            p[0] = f32x4{v[0], v[1], v[2], v[3]};
+            p[1] = f32x4{v[4], v[5], v[6], v[7]};
+        } else {
+            u16x8 u;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) u[i] = f32_to_half<DT>(v[i]);
+            *reinterpret_cast<u16x8*>(static_cast<uint16_t*>(base) + e) = u;
+        }
+    }
+    // Bit-exact copy of 8 elements.
+    __device__ __forceinline__ static void copy(const void* src, int64_t es, void* dst, int64_t ed) {
+        if constexpr (DT == kF32) {
+            const u32x4* p = reinterpret_cast<const u32x4*>(static_cast<const float*>(src) + es);
+            u32x4* q = reinterpret_cast<u32x4*>(static_cast<float*>(dst) + ed);
+            q[0] = p[0];
+            q[1] = p[1];
+        } else {
+            *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(dst) + ed) =
+                *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(src) + es);
+        }
+    }
+};
+
+__device__ __forceinline__ void load_centroid8(const float* c, float (&v)[8]) {
+    const f32x4 a = reinterpret_cast<const f32x4*>(c)[0];
+    const f32x4 b = reinterpret_cast<const f32x4*>(c)[1];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { v[i] = a[i]; v[4 + i] = b[i]; }
+}
+
+// Quantize 8 residual channels of one token held by this lane; the lane group of G lanes
+// together holds the whole token. Returns codes, writes xhat, low and scale.
+template <int G>
+__device__ __forceinline__ void base_offset_lane(const float (&x)[8], const float (&c)[8], float levels,
+                                                 float (&xhat)[8], uint8_t (&code)[8], float& low_out,
+                                                 float& scale_out) {
+    float r[8];
+    float lo = INFINITY, hi = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        r[i] = x[i] - c[i];
+        lo = fminf(lo, r[i]);
+        hi = fmaxf(hi, r[i]);
+    }
+#pragma unroll
+    for (int m = 1; m < G; m <<= 1) {
+        lo = fminf(lo, __shfl_xor(lo, m, G));
+        hi = fmaxf(hi, __shfl_xor(hi, m, G));
+    }
+    const float span = hi - lo;
+    const float raw = span / levels;
+    const float scale = raw > 0.0f ? raw : 1.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float shifted = r[i] - lo;
+        float q = __builtin_rintf(shifted / scale);
+        q = q < 0.0f ? 0.0f : (q > levels ? levels : q);
+        code[i] = static_cast<uint8_t>(q);
+        const float step = scale * static_cast<float>(code[i]);
+        const float resid = lo + step;
+        xhat[i] = c[i] + resid;
+    }
+    low_out = lo;
+    scale_out = scale;
+}
+
+template <int DT, int G>
+__global__ __launch_bounds__(256) void base_offset_kernel(const void* __restrict__ x, const int32_t* __restrict__ labels,
+                                                          const float* __restrict__ centroids, int64_t rows,
+                                                          int tokens, int clusters, int bits,
+                                                          uint8_t* __restrict__ codes, float* __restrict__ low,
+                                                          float* __restrict__ scale, void* __restrict__ xhat) {
+    constexpr int D = G * 8;
+    const int sub = threadIdx.x % G;
+    const float levels = static_cast<float>((1 << bits) - 1);
+    for (int64_t row = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / G; row < rows;
+         row += static_cast<int64_t>(gridDim.x) * blockDim.x / G) {
+        const int64_t b = row / tokens;
+        const int lab = labels[row];
+        float xv[8], cv[8], out[8], lo, sc;
+        uint8_t q[8];
+        Row8<DT>::load(x, row * D + sub * 8, xv);
+        load_centroid8(centroids + (b * clusters + lab) * D + sub * 8, cv);
+        base_offset_lane<G>(xv, cv, levels, out, q, lo, sc);
+        if (codes) {
+            u32x2 packed;
+            packed[0] = q[0] | (q[1] << 8) | (q[2] << 16) | (static_cast<uint32_t>(q[3]) << 24);
+            packed[1] = q[4] | (q[5] << 8) | (q[6] << 16) | (static_cast<uint32_t>(q[7]) << 24);
+            *reinterpret_cast<u32x2*>(codes + row * D + sub * 8) = packed;
+        }
+        if (sub == 0) {
+            if (low) low[row] = lo;
+            if (scale) scale[row] = sc;
+        }
+        if (xhat) Row8<DT>::store(xhat, row * D + sub * 8, out);
+    }
+}
+
+template <int DT, int G>
+__global__ __launch_bounds__(256) void base_offset_decode_kernel(const uint8_t* __restrict__ codes,
+                                                                 const float* __restrict__ low,
+                                                                 const float* __restrict__ scale,
+                                                                 const int32_t* __restrict__ labels,
+                                                                 const float* __restrict__ centroids, int64_t rows,
+                                                                 int tokens, int clusters, void* __restrict__ xhat) {
+    constexpr int D = G * 8;
+    const int sub = threadIdx.x % G;
+    for (int64_t row = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / G; row < rows;
+         row += static_cast<int64_t>(gridDim.x) * blockDim.x / G) {
+        const int64_t b = row / tokens;
+        float cv[8], out[8];
+        load_centroid8(centroids + (b * clusters + labels[row]) * D + sub * 8, cv);
+        const u32x2 packed = *reinterpret_cast<const u32x2*>(codes + row * D + sub * 8);
+        const float lo = low[row], sc = scale[row];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t code = (packed[i / 4] >> (8 * (i % 4))) & 0xffu;
+            const float step = sc * static_cast<float>(code);
+            const float resid = lo + step;
+            out[i] = cv[i] + resid;
+        }
+        Row8<DT>::store(xhat, row * D + sub * 8, out);
+    }
+}
+
+}  // namespace
+
+struct PackTensor {
+    const void* input;        // [batch, length, dims]
+    void* output;             // [batch, length, dims]
+    const int32_t* indices;   // [batch, video]: original video token at each packed position
+    const int32_t* labels;    // [batch, video] (read only when bits != 0)
+    const float* centroids;   // [batch, clusters, dims] (read only when bits != 0)
+    int clusters;
+    int bits;                 // 0 = plain gather, 4 or 8 = fake-quantize while gathering
+};
+
+struct PackArgs {
+    PackTensor t[3];
+    int num, batch, length, video;
+};
+
+namespace {
+
+template <int DT, int G>
+__global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
+    constexpr int D = G * 8;
+    const int sub = threadIdx.x % G;
+    const int64_t per_tensor = static_cast<int64_t>(a.batch) * a.length;
+    const int64_t rows = per_tensor * a.num;
+    for (int64_t r = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / G; r < rows;
+         r += static_cast<int64_t>(gridDim.x) * blockDim.x / G) {
+        const int ti = static_cast<int>(r / per_tensor);
+        const PackTensor& T = a.t[ti];
+        const int64_t row = r - ti * per_tensor;
+        const int64_t b = row / a.length;
+        const int j = static_cast<int>(row - b * a.length);
+        const int64_t dst = row * D + sub * 8;
+        if (j >= a.video) {
+            Row8<DT>::copy(T.input, dst, T.output, dst);
+            continue;
+        }
+        const int tok = T.indices[b * a.video + j];
+        const int64_t src = (b * a.length + tok) * D + sub * 8;
+        if (T.bits == 0) {
+            Row8<DT>::copy(T.input, src, T.output, dst);
+            continue;
+        }
+        const int lab = T.labels[b * a.video + tok];
+        float xv[8], cv[8], out[8], lo, sc;
+        uint8_t q[8];
+        Row8<DT>::load(T.input, src, xv);
+        load_centroid8(T.centroids + (b * T.clusters + lab) * D + sub * 8, cv);
+        base_offset_lane<G>(xv, cv, static_cast<float>((1 << T.bits) - 1), out, q, lo, sc);
+        Row8<DT>::store(T.output, dst, out);
+    }
+}
+
+int grid_for_rows(int64_t rows, int G) {
+    const int64_t threads = rows * G;
+    return static_cast<int>(std::min<int64_t>(ceil_div(threads, 256), 1 << 20));
+}
+
+template <template <int, int> class K, typename... Args>
+bool dispatch_dt_g(int dtype, int dims, int64_t rows, hipStream_t s, Args... args) {
+#define PECO_LAUNCH(DT_, G_)                                                                             \
+    hipLaunchKernelGGL((K<DT_, G_>::kernel), dim3(grid_for_rows(rows, G_)), dim3(256), 0, s, args...); \
+    return true;
+    const int G = dims / 8;
+    if (dtype == kBF16) {
+        if (G == 16) { PECO_LAUNCH(kBF16, 16) }
+        if (G == 8) { PECO_LAUNCH(kBF16, 8) }
+    } else if (dtype == kF16) {
+        if (G == 16) { PECO_LAUNCH(kF16, 16) }
+        if (G == 8) { PECO_LAUNCH(kF16, 8) }
+    } else if (dtype == kF32) {
+        if (G == 16) { PECO_LAUNCH(kF32, 16) }
+        if (G == 8) { PECO_LAUNCH(kF32, 8) }
+    }
+#undef PECO_LAUNCH
+    return false;
+}
+
+template <int DT, int G> struct EncodeK { static constexpr auto kernel = base_offset_kernel<DT, G>; };
+template <int DT, int G> struct DecodeK { static constexpr auto kernel = base_offset_decode_kernel<DT, G>; };
+template <int DT, int G> struct PackK { static constexpr auto kernel = pack_kernel<DT, G>; };
+
+bool valid_quant_args(int batch, int tokens, int clusters, int dims) {
+    return batch >= 1 && tokens >= 1 && clusters >= 1 && (dims == 64 || dims == 128);
+}
+
+}  // namespace
+}  // namespace peco
+
+using namespace peco;
+
+PECO_API int peco_base_offset_encode(const void* x, int dtype, const int32_t* labels, const float* centroids,
+                                     int batch, int tokens, int clusters, int dims, int bits, uint8_t* codes,
+                                     float* low, float* scale, void* stream) {
+    if (!x || !labels || !centroids || !valid_quant_args(batch, tokens, clusters, dims) || (bits != 4 && bits != 8))
+        return kInvalidValue;
+    const int64_t rows = static_cast<int64_t>(batch) * tokens;
+    if (!dispatch_dt_g<EncodeK>(dtype, dims, rows, static_cast<hipStream_t>(stream), x, labels, centroids, rows,
+                                tokens, clusters, bits, codes, low, scale, static_cast<void*>(nullptr)))
+        return kUnsupportedDtype;
+    return hipGetLastError();
+}
+
+PECO_API int peco_base_offset_decode(const uint8_t* codes, const float* low, const float* scale,
+                                     const int32_t* labels, const float* centroids, int batch, int tokens,
+                                     int clusters, int dims, int dtype, void* out, void* stream) {
+    if (!codes || !low || !scale || !labels || !centroids || !out || !valid_quant_args(batch, tokens, clusters, dims))
+        return kInvalidValue;
+    const int64_t rows = static_cast<int64_t>(batch) * tokens;
+    if (!dispatch_dt_g<DecodeK>(dtype, dims, rows, static_cast<hipStream_t>(stream), codes, low, scale, labels,
+                                centroids, rows, tokens, clusters, out))
+        return kUnsupportedDtype;
+    return hipGetLastError();
+}
+
+PECO_API int peco_base_offset_fake_quant(const void* x, int dtype, const int32_t* labels, const float* centroids,
+                                         int batch, int tokens, int clusters, int dims, int bits, void* out,
+                                         void* stream) {
+    if (!x || !labels || !centroids || !out || !valid_quant_args(batch, tokens, clusters, dims) ||
+        (bits != 4 && bits != 8))
+        return kInvalidValue;
+    const int64_t rows = static_cast<int64_t>(batch) * tokens;
+    if (!dispatch_dt_g<EncodeK>(dtype, dims, rows, static_cast<hipStream_t>(stream), x, labels, centroids, rows,
+                                tokens, clusters, bits, static_cast<uint8_t*>(nullptr), static_cast<float*>(nullptr),
+                                static_cast<float*>(nullptr), out))
+        return kUnsupportedDtype;
+    return hipGetLastError();
+}
+
+// One launch packs up to three tensors (Q, K, V) of shape [batch, length, dims]:
+// rows [0, video) are gathered in cluster order (optionally fake-quantized),
+// rows [video, length) (text) are copied in place.
+PECO_API int peco_pack_clustered(const void* const* inputs, void* const* outputs, const int32_t* const* indices,
+                                 const int32_t* const* labels, const float* const* centroids, const int* clusters,
+                                 const int* bits, int num_tensors, int batch, int length, int video, int dims,
+                                 int dtype, void* stream) {
+    if (num_tensors < 1 || num_tensors > 3 || batch < 1 || length < 1 || video < 0 || video > length ||
+        (dims != 64 && dims != 128))
+        return kInvalidValue;
+    PackArgs a{};
+    a.num = num_tensors;
+    a.batch = batch;
+    a.length = length;
+    a.video = video;
+    for (int i = 0; i < num_tensors; ++i) {
+        if (!inputs[i] || !outputs[i] || (video > 0 && !indices[i])) return kInvalidValue;
+        if (bits[i] != 0 && bits[i] != 4 && bits[i] != 8) return kInvalidValue;
+        if (bits[i] != 0 && (!labels[i] || !centroids[i] || clusters[i] < 1)) return kInvalidValue;
+        a.t[i] = PackTensor{inputs[i], outputs[i], indices[i], labels[i], centroids[i], clusters[i], bits[i]};
+    }
+    const int64_t rows = static_cast<int64_t>(num_tensors) * batch * length;
+    if (!dispatch_dt_g<PackK>(dtype, dims, rows, static_cast<hipStream_t>(stream), a)) return kUnsupportedDtype;
+    return hipGetLastError();
+}

@@ -1,0 +1,265 @@
+// Stage 3: stable cluster sort of token labels, and row gather/scatter by permutation.
+//
+// The permutation is the stable argsort of labels per batch entry
+// (peco/clustering.py:105, torch.argsort(..., stable=True)), computed as a counting sort:
+//   1. sort_hist:  per 1024-token tile, a label histogram (LDS atomics; counts only).
+//   2. sort_scan:  per batch entry, scan tiles per cluster and clusters -> absolute
+//                  start position of each (tile, cluster) run, counts and offsets.
+//   3. sort_place: per tile, one wavefront ranks 64 tokens per step. Lanes holding the
+//                  same label are found with one ballot per label bit (no serial match
+//                  loop); the rank among equal labels is a popcount of lower lanes, so
+//                  original order is kept within each cluster.
+// Reordering copies rows of dims*item_size bytes with 16-byte lanes where alignment
+// allows (peco/kernels/kmeans.cu:92-107 is the reference's 2/4-byte-per-thread copy).
+#include "sort.hpp"
+
+#include <algorithm>
+
+namespace peco {
+namespace {
+
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const int y = __shfl_up(v, d, kWave);
+        if (lane >= d) v += y;
+    }
+    return v;
+}
+
+// Exclusive scan across a 256-thread block; returns the exclusive prefix and the total.
+__device__ __forceinline__ int block_exclusive_scan256(int v, int* tmp, int* total) {
+    const int lane = lane_id();
+    const int wave = threadIdx.x / kWave;
+    const int inc = wave_inclusive_scan(v);
+    if (lane == kWave - 1) tmp[wave] = inc;
+    __syncthreads();
+    int base = 0, sum = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const int t = tmp[w];
+        base += w < wave ? t : 0;
+        sum += t;
+    }
+    __syncthreads();
+    *total = sum;
+    return base + inc - v;
+}
+
+__device__ __forceinline__ int find_problem_by_block(const SortArgs& a, int block) {
+    int p = 0;
+    while (p + 1 < a.num && block >= a.p[p + 1].block_begin) ++p;
+    return p;
+}
+
+__device__ __forceinline__ int find_problem_by_batch(const SortArgs& a, int b) {
+    int p = 0;
+    while (p + 1 < a.num && b >= a.p[p + 1].batch_begin) ++p;
+    return p;
+}
+
+__global__ __launch_bounds__(256) void sort_hist_kernel(SortArgs args) {
+    extern __shared__ int hist[];
+    const int pi = find_problem_by_block(args, blockIdx.x);
+    const SortProblem& P = args.p[pi];
+    const int local = blockIdx.x - P.block_begin;
+    const int b = local / P.tiles;
+    const int tile = local % P.tiles;
+    for (int k = threadIdx.x; k < P.clusters; k += blockDim.x) hist[k] = 0;
+    __syncthreads();
+    const int32_t* lab = P.labels + static_cast<int64_t>(b) * P.tokens;
+    const int begin = tile * kSortTile;
+    const int end = min(P.tokens, begin + kSortTile);
+    for (int t = begin + threadIdx.x; t < end; t += blockDim.x) {
+        const int L = lab[t];
+        if (static_cast<unsigned>(L) < static_cast<unsigned>(P.clusters)) atomicAdd(&hist[L], 1);
+    }
+    __syncthreads();
+    int32_t* out = P.tile_hist + (static_cast<int64_t>(b) * P.tiles + tile) * P.clusters;
+    for (int k = threadIdx.x; k < P.clusters; k += blockDim.x) out[k] = hist[k];
+}
+
+__global__ __launch_bounds__(256) void sort_scan_kernel(SortArgs args) {
+    extern __shared__ int cnt[];
+    __shared__ int tmp[4];
+    const int pi = find_problem_by_batch(args, blockIdx.x);
+    const SortProblem& P = args.p[pi];
+    const int b = blockIdx.x - P.batch_begin;
+    const int K = P.clusters;
+    int32_t* th = P.tile_hist + static_cast<int64_t>(b) * P.tiles * K;
+    for (int k = threadIdx.x; k < K; k += blockDim.x) {
+        int run = 0;
+        for (int tile = 0; tile < P.tiles; ++tile) {
+            const int c = th[static_cast<int64_t>(tile) * K + k];
+            th[static_cast<int64_t>(tile) * K + k] = run;
+            run += c;
+        }
+        cnt[k] = run;
+    }
+    __syncthreads();
+    // Exclusive scan over clusters: each thread owns a contiguous chunk.
+    const int per = static_cast<int>(ceil_div(K, blockDim.x));
+    const int k0 = threadIdx.x * per;
+    const int k1 = min(K, k0 + per);
+    int local = 0;
+    for (int k = k0; k < k1; ++k) local += cnt[k];
+    int total = 0;
+    int run = block_exclusive_scan256(local, tmp, &total);
+    int32_t* off = P.offsets + static_cast<int64_t>(b) * (K + 1);
+    int32_t* counts = P.counts ? P.counts + static_cast<int64_t>(b) * K : nullptr;
+    for (int k = k0; k < k1; ++k) {
+        const int c = cnt[k];
+        off[k] = run;
+        if (counts) counts[k] = c;
+        for (int tile = 0; tile < P.tiles; ++tile) th[static_cast<int64_t>(tile) * K + k] += run;
+        run += c;
+    }
+    if (threadIdx.x == 0) off[K] = total;
+}
+
+__global__ __launch_bounds__(64) void sort_place_kernel(SortArgs args) {
+    extern __shared__ int base[];
+    const int pi = find_problem_by_block(args, blockIdx.x);
+    const SortProblem& P = args.p[pi];
+    const int local = blockIdx.x - P.block_begin;
+    const int b = local / P.tiles;
+    const int tile = local % P.tiles;
+    const int K = P.clusters;
+    const int lane = threadIdx.x;
+    const int32_t* th = P.tile_hist + (static_cast<int64_t>(b) * P.tiles + tile) * K;
+    int32_t* th_mut = P.tile_hist + (static_cast<int64_t>(b) * P.tiles + tile) * K;
+    for (int k = lane; k < K; k += kWave) {
+        base[k] = th[k];
+        if (args.zero_hist) th_mut[k] = 0;
+    }
+    __syncthreads();
+    const int bits = K > 1 ? 32 - __builtin_clz(static_cast<unsigned>(K - 1)) : 0;
+    const int32_t* lab = P.labels + static_cast<int64_t>(b) * P.tokens;
+    int32_t* idx = P.indices + static_cast<int64_t>(b) * P.tokens;
+    int32_t* ranks = P.ranks ? P.ranks + static_cast<int64_t>(b) * P.tokens : nullptr;
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
+    const int begin = tile * kSortTile;
+    const int end = min(P.tokens, begin + kSortTile);
+    for (int step = begin; step < end; step += kWave) {
+        const int t = step + lane;
+        const int raw = t < end ? lab[t] : 0;
+        const bool active = t < end && static_cast<unsigned>(raw) < static_cast<unsigned>(K);
+        const int L = active ? raw : 0;
+        uint64_t eq = __ballot(active);
+        for (int bit = 0; bit < bits; ++bit) {
+            const bool on = active && ((L >> bit) & 1);
+            const uint64_t m = __ballot(on);
+            eq &= ((L >> bit) & 1) ? m : ~m;
+        }
+        const int rank = __popcll(eq & below);
+        const int total = __popcll(eq);
+        const bool last = active && ((eq >> lane) == 1ull);
+        if (active) {
+            const int pos = base[L] + rank;
+            idx[pos] = t;
+            if (ranks) ranks[t] = pos;
+        }
+        __syncthreads();
+        if (last) base[L] += total;
+        __syncthreads();
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void reorder_rows_kernel(const T* __restrict__ in, const int32_t* __restrict__ idx,
+                                                           T* __restrict__ out, int tokens, int chunks,
+                                                           int64_t total, int inverse) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t row = i / chunks;
+        const int c = static_cast<int>(i - row * chunks);
+        const int64_t head = row / tokens;
+        const int tok = idx[row];
+        if (static_cast<unsigned>(tok) >= static_cast<unsigned>(tokens)) continue;
+        const int64_t mapped = (head * tokens + tok) * chunks + c;
+        if (inverse) out[mapped] = in[i];
+        else out[i] = in[mapped];
+    }
+}
+
+}  // namespace
+
+void sort_args_finalize(SortArgs& a) {
+    int blocks = 0, batches = 0;
+    for (int i = 0; i < a.num; ++i) {
+        a.p[i].tiles = sort_tiles(a.p[i].tokens);
+        a.p[i].block_begin = blocks;
+        a.p[i].batch_begin = batches;
+        blocks += a.p[i].batch * a.p[i].tiles;
+        batches += a.p[i].batch;
+    }
+    a.total_blocks = blocks;
+    a.total_batches = batches;
+}
+
+hipError_t launch_cluster_sort(const SortArgs& args, hipStream_t stream, bool with_hist) {
+    int kmax = 1;
+    for (int i = 0; i < args.num; ++i) kmax = max(kmax, args.p[i].clusters);
+    const size_t lds = sizeof(int) * static_cast<size_t>(kmax);
+    if (with_hist) hipLaunchKernelGGL(sort_hist_kernel, dim3(args.total_blocks), dim3(256), lds, stream, args);
+    hipLaunchKernelGGL(sort_scan_kernel, dim3(args.total_batches), dim3(256), lds, stream, args);
+    hipLaunchKernelGGL(sort_place_kernel, dim3(args.total_blocks), dim3(64), lds, stream, args);
+    return hipGetLastError();
+}
+
+}  // namespace peco
+
+using namespace peco;
+
+PECO_API size_t peco_cluster_sort_workspace_size(int batch, int tokens, int clusters) {
+    if (batch < 1 || tokens < 1 || clusters < 1) return 0;
+    return sizeof(int32_t) * (sort_workspace_ints(batch, tokens, clusters) + static_cast<size_t>(batch) * (clusters + 1));
+}
+
+PECO_API int peco_cluster_sort(const int32_t* labels, int batch, int tokens, int clusters, int32_t* indices,
+                               int32_t* ranks, int32_t* counts, int32_t* offsets, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+    if (!labels || !indices || batch < 1 || tokens < 1 || clusters < 1 || clusters > kMaxSortClusters)
+        return kInvalidValue;
+    if (workspace_bytes < peco_cluster_sort_workspace_size(batch, tokens, clusters) || !workspace)
+        return kWorkspaceTooSmall;
+    SortArgs a{};
+    a.num = 1;
+    SortProblem& p = a.p[0];
+    p.labels = labels;
+    p.indices = indices;
+    p.ranks = ranks;
+    p.counts = counts;
+    p.tile_hist = static_cast<int32_t*>(workspace);
+    p.offsets = offsets ? offsets : p.tile_hist + sort_workspace_ints(batch, tokens, clusters);
+    p.batch = batch;
+    p.tokens = tokens;
+    p.clusters = clusters;
+    sort_args_finalize(a);
+    return launch_cluster_sort(a, static_cast<hipStream_t>(stream), true);
+}
+
+PECO_API int peco_reorder_token_features(const void* input, const int32_t* indices, void* output, int batch_heads,
+                                         int tokens, int dims, int item_size, int inverse, void* stream) {
+    if (!input || !indices || !output || batch_heads < 1 || tokens < 0 || dims < 1 ||
+        (item_size != 2 && item_size != 4))
+        return kInvalidValue;
+    if (tokens == 0) return kOk;
+    const int64_t row_bytes = static_cast<int64_t>(dims) * item_size;
+    const uintptr_t align = reinterpret_cast<uintptr_t>(input) | reinterpret_cast<uintptr_t>(output);
+    const int64_t rows = static_cast<int64_t>(batch_heads) * tokens;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    auto launch = [&](auto tag, int width) {
+        using T = decltype(tag);
+        const int chunks = static_cast<int>(row_bytes / width);
+        const int64_t total = rows * chunks;
+        const int blocks = static_cast<int>(std::min<int64_t>(ceil_div(total, 256), 1 << 20));
+        hipLaunchKernelGGL(reorder_rows_kernel<T>, dim3(blocks), dim3(256), 0, s, static_cast<const T*>(input),
+                           indices, static_cast<T*>(output), tokens, chunks, total, inverse);
+    };
+    if (row_bytes % 16 == 0 && align % 16 == 0) launch(u32x4{}, 16);
+    else if (row_bytes % 4 == 0 && align % 4 == 0) launch(uint32_t{}, 4);
+    else launch(uint16_t{}, 2);
+    return hipGetLastError();
+}

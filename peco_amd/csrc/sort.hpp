@@ -1,0 +1,47 @@
+// Stable counting sort of cluster labels (host-side launch interface).
+#pragma once
+
+#include "common.hpp"
+
+namespace peco {
+
+// Tokens per sort tile: one tile is ranked by a single wavefront, 64 tokens per step.
+constexpr int kSortTile = 1024;
+constexpr int kMaxSortClusters = 16384;
+
+struct SortProblem {
+    const int32_t* labels;  // [batch, tokens], values in [0, clusters)
+    int32_t* indices;       // [batch, tokens]: original token at each sorted position
+    int32_t* ranks;         // nullable [batch, tokens]: sorted position of each token
+    int32_t* counts;        // nullable [batch, clusters]
+    int32_t* offsets;       // [batch, clusters + 1]: first sorted position of each cluster
+    int32_t* tile_hist;     // workspace [batch, tiles, clusters]
+    int batch, tokens, clusters, tiles;
+    int block_begin;        // first linear (batch, tile) block of this problem
+    int batch_begin;        // first linear batch entry of this problem (scan grid)
+};
+
+constexpr int kMaxSortProblems = 2;
+
+struct SortArgs {
+    SortProblem p[kMaxSortProblems];
+    int num;
+    int total_blocks;   // sum of batch * tiles
+    int total_batches;  // sum of batch
+    int zero_hist;      // sort_place clears each consumed tile histogram (for accumulating producers)
+};
+
+inline int sort_tiles(int tokens) { return static_cast<int>(ceil_div(tokens, kSortTile)); }
+
+inline size_t sort_workspace_ints(int batch, int tokens, int clusters) {
+    return static_cast<size_t>(batch) * sort_tiles(tokens) * clusters;
+}
+
+// Fills block_begin/batch_begin/totals for problems[0..num).
+void sort_args_finalize(SortArgs& args);
+
+// with_hist=false: tile_hist already holds the per-tile label counts (e.g. accumulated
+// by the k-means assign kernel), so only the scan and place kernels run.
+hipError_t launch_cluster_sort(const SortArgs& args, hipStream_t stream, bool with_hist);
+
+}  // namespace peco

@@ -1,0 +1,79 @@
+"""End-to-end GPU parity of PecoAttention.attention against the oracle's reference path."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import canonical, reference_path
+from peco_amd import processor, workloads
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _run_layer(wl, iterations):
+    shape = wl.shape
+    cfg = processor.PecoConfig(num_q_centroids=shape.num_q_centroids, num_k_centroids=shape.num_k_centroids,
+                               top_p=wl.top_p, min_kc_ratio=wl.min_kc_ratio, kmeans_iter_init=iterations,
+                               kmeans_iter_step=iterations, warmup_steps=0, base_offset_bits=shape.bits)
+    ctx = processor.InferenceContext(step=0, text_length=shape.text, valid_text_length=shape.text)
+    layer = processor.PecoAttention(0, cfg, ctx)
+    layer.q_centroids, layer.k_centroids = wl.q_init.to(DEV), wl.k_init.to(DEV)
+    with torch.no_grad():
+        out = layer.attention(wl.query.to(DEV), wl.key.to(DEV), wl.value.to(DEV))
+    torch.cuda.synchronize()
+    return layer, out
+
+
+def _oracle_layer(wl, iterations):
+    shape = wl.shape
+
+    def attend(q, k, v, m, qs, ks):
+        o = canonical.sparse_attention(q[0].float().numpy(), k[0].float().numpy(), v[0].float().numpy(),
+                                       m[0].numpy(), qs[0].numpy(), ks[0].numpy())
+        return torch.from_numpy(o)[None]
+
+    def fit(x, clusters, iters, init):
+        labels, centers, counts, _, _ = canonical.kmeans_fit(x.float().numpy(), init.numpy(), iters)
+        return torch.from_numpy(labels), torch.from_numpy(centers), torch.from_numpy(counts), iters
+
+    stages = {}
+    out = reference_path.peco_layer(
+        wl.query, wl.key, wl.value, num_q_centroids=shape.num_q_centroids, num_k_centroids=shape.num_k_centroids,
+        iterations=iterations, q_init=wl.q_init, k_init=wl.k_init, top_p=wl.top_p, min_kc_ratio=wl.min_kc_ratio,
+        bits=shape.bits, text_length=shape.text, valid_text=shape.text, attention=attend, fit=fit, stages=stages)
+    return out, stages
+
+
+@pytest.mark.parametrize("name,heads,video", [
+    ("hunyuan_480p", 2, 6750),
+    ("hunyuan_480p_bo4", 2, 6750),
+    ("cpu_small", 2, 2048),
+])
+def test_layer_matches_oracle(announce, name, heads, video):
+    wl = workloads.make_workload(name, heads=heads, video=video)
+    if wl.query.dtype == torch.float32:
+        # The sparse attention kernel takes fp16/bf16 (as the reference's); run the fp32
+        # workload in bf16 end to end.
+        wl = workloads.Workload(wl.shape, wl.query.bfloat16(), wl.key.bfloat16(), wl.value.bfloat16(),
+                                wl.q_init, wl.k_init)
+    iters = wl.shape.iterations
+    announce(f"{name} heads={heads} video={video} iters={iters}")
+    layer, out = _run_layer(wl, iters)
+    ref, st = _oracle_layer(wl, iters)
+    # Stage 1 + 3: labels and permutations are bit-exact.
+    n = wl.shape.video
+    q_idx, k_idx = layer._last_fit
+    xq = wl.query[0, :, :n].float().numpy()
+    rl, rc, _, ridx, _ = canonical.kmeans_fit(xq, wl.q_init.numpy(), iters)
+    assert np.array_equal(q_idx.cpu().numpy(), ridx)
+    assert np.array_equal(layer.q_centroids.cpu().numpy().view(np.int32), rc.view(np.int32))
+    # The torch-literal k-means of the reference path agrees with the canonical labels
+    # except at near-ties (its bmm summation order is MKL's).
+    tl, _, _, _ = reference_path.fit_token_clusters(torch.from_numpy(xq), wl.shape.num_q_centroids, iters, wl.q_init)
+    agree = (tl.numpy() == rl).mean()
+    assert agree > 0.99, f"reference-path label agreement {agree}"
+    err = (out.float().cpu() - ref.float()).abs()
+    print(f"[layer] {name}: max {err.max().item():.3e} mean {err.mean().item():.3e} "
+          f"label agreement {agree:.6f}", flush=True)
+    assert err.mean().item() <= 2e-3
+    assert err.max().item() <= 2e-2

@@ -1,0 +1,284 @@
+"""GPU parity of each hot-path stage against the CPU oracle (bit-exact where integer/byte).
+
+Every test feeds the HIP kernel and the oracle the same seeded inputs. Integer and byte
+results (labels, permutations, counts, codes) and the fixed-order fp32 results (centres,
+norms, Base-Offset reconstructions) must match bit for bit; attention output must be
+within max-abs 2e-2 and mean-abs 2e-3 of the float64 oracle.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import canonical, reference_path
+from peco_amd import attention_cuda, clustering, clustering_cuda, quantization
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _gen(seed):
+    g = torch.Generator()
+    g.manual_seed(seed)
+    return g
+
+
+def _mixture(g, bh, n, d, m, sigma=1.0):
+    means = torch.randn(bh, m, d, generator=g)
+    means = means / means.norm(dim=-1, keepdim=True) * 8.0
+    comp = torch.randint(m, (bh, n), generator=g)
+    return means.gather(1, comp[..., None].expand(-1, -1, d)) + sigma * torch.randn(bh, n, d, generator=g)
+
+
+# ---------------------------------------------------------------- stage 3: sort + reorder
+
+@pytest.mark.parametrize("clusters,tokens", [(1, 777), (7, 5000), (256, 6750), (1000, 3000), (64, 70)])
+def test_cluster_sort_matches_stable_argsort(announce, clusters, tokens):
+    g = _gen(clusters * 31 + tokens)
+    labels = torch.randint(clusters, (3, tokens), generator=g, dtype=torch.int32)
+    announce(f"K={clusters} N={tokens}")
+    idx, counts, offsets = clustering_cuda.cluster_sort(labels.to(DEV), clusters)
+    ref_idx, ref_off = canonical.stable_sort(labels.numpy(), clusters)
+    assert np.array_equal(idx.cpu().numpy(), ref_idx)
+    assert np.array_equal(offsets.cpu().numpy(), ref_off)
+    assert np.array_equal(counts.cpu().numpy(), np.diff(ref_off, axis=1))
+    torch_idx = torch.argsort(labels, dim=-1, stable=True).to(torch.int32)
+    assert torch.equal(idx.cpu(), torch_idx)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("dims", [64, 128, 40])
+def test_reorder_roundtrip_bit_exact(announce, dtype, dims):
+    g = _gen(dims)
+    x = torch.randn(1, 3, 513, dims, generator=g).to(dtype)
+    perm = torch.stack([torch.randperm(513, generator=g) for _ in range(3)]).to(torch.int32)
+    announce(f"{dtype} D={dims}")
+    xd, pd = x.to(DEV), perm.to(DEV)
+    fwd = clustering_cuda.reorder_token_features(xd, pd)
+    inv = clustering_cuda.reorder_token_features(fwd, pd, inverse=True)
+    ref = reference_path.gather_tokens(x, perm)
+    assert torch.equal(fwd.cpu().view(torch.int16 if dtype != torch.float32 else torch.int32),
+                       ref.view(torch.int16 if dtype != torch.float32 else torch.int32))
+    assert torch.equal(inv.cpu(), x)
+    assert torch.equal(clustering.restore_sequence_order(fwd, pd).cpu(), x)
+
+
+# ---------------------------------------------------------------- stage 2: Base-Offset
+
+def _bits_equal(a, b):
+    a, b = a.contiguous(), b.contiguous()
+    if a.dtype in (torch.bfloat16, torch.float16):
+        return torch.equal(a.view(torch.int16), b.view(torch.int16))
+    if a.dtype == torch.float32:
+        return torch.equal(a.view(torch.int32), b.view(torch.int32))
+    return torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("dims", [128, 64])
+def test_base_offset_bit_exact(announce, dtype, bits, dims):
+    g = _gen(bits * 7 + dims)
+    bh, n, k = 3, 1500, 24
+    x = _mixture(g, bh, n, dims, 8).to(dtype)
+    cent = torch.randn(bh, k, dims, generator=g) * 2
+    labels = torch.randint(k, (bh, n), generator=g, dtype=torch.int32)
+    # A constant-residual token (scale falls back to 1) and a token equal to its centroid.
+    x[0, 0] = (cent[0, labels[0, 0]] + 0.5).to(dtype)
+    cent[1, labels[1, 3]] = x[1, 3].float()
+    announce(f"{dtype} bits={bits} D={dims}")
+    enc = quantization.quantize_base_offset(x.to(DEV), labels.to(DEV), cent.to(DEV), bits)
+    codes, low, scale, xhat = canonical.base_offset(x.float().numpy(), labels.numpy(), cent.numpy(), bits)
+    assert np.array_equal(enc.codes.cpu().numpy(), codes)
+    assert np.array_equal(enc.offset_min.cpu().numpy()[..., 0].view(np.int32), low.view(np.int32))
+    assert np.array_equal(enc.scale.cpu().numpy()[..., 0].view(np.int32), scale.view(np.int32))
+    ref_hat = torch.from_numpy(xhat).to(dtype)
+    assert _bits_equal(enc.dequantize().cpu(), ref_hat)
+    fq = quantization.fake_quantize_base_offset(x.to(DEV), labels.to(DEV), cent.to(DEV), bits)
+    assert _bits_equal(fq.cpu(), ref_hat)
+    # The torch restatement of the reference gives the same bits.
+    assert _bits_equal(reference_path.fake_quantize(x, labels, cent, bits), ref_hat)
+
+
+@pytest.mark.parametrize("bits", [0, 4])
+def test_pack_matches_quant_gather_concat(announce, bits):
+    g = _gen(bits + 100)
+    h, n, t, d, kq, kk = 3, 900, 40, 128, 12, 30
+    q = _mixture(g, h, n + t, d, 6).to(torch.bfloat16)[None]
+    k = _mixture(g, h, n + t, d, 6).to(torch.bfloat16)[None]
+    v = torch.randn(1, h, n + t, d, generator=g).to(torch.bfloat16)
+    ql = torch.randint(kq, (h, n), generator=g, dtype=torch.int32)
+    kl = torch.randint(kk, (h, n), generator=g, dtype=torch.int32)
+    qc = torch.randn(h, kq, d, generator=g)
+    kc = torch.randn(h, kk, d, generator=g)
+    qi = reference_path.stable_indices(ql)
+    ki = reference_path.stable_indices(kl)
+    announce(f"bits={bits}")
+    outs = clustering_cuda.pack_clustered(
+        [q.to(DEV), k.to(DEV), v.to(DEV)], [qi.to(DEV), ki.to(DEV), ki.to(DEV)], [ql.to(DEV), kl.to(DEV), None],
+        [qc.to(DEV), kc.to(DEV), None], [bits, bits, 0], n)
+    for out, x, lab, cent, idx in ((outs[0], q, ql, qc, qi), (outs[1], k, kl, kc, ki), (outs[2], v, None, None, ki)):
+        video = x[:, :, :n]
+        if lab is not None:
+            video = reference_path.fake_quantize(video, lab, cent, bits).reshape(video.shape)
+        ref = torch.cat((reference_path.gather_tokens(video, idx), x[:, :, n:]), 2)
+        assert _bits_equal(out.cpu(), ref)
+
+
+# ---------------------------------------------------------------- stage 1: k-means
+
+def _centres_with_duplicates(g, x, k):
+    bh, n, d = x.shape
+    idx = torch.randint(n, (bh, k), generator=g)
+    idx[:, 1] = idx[:, 0]  # guaranteed duplicate centre -> exact tie, lowest id wins
+    return x.float().gather(1, idx[..., None].expand(-1, -1, d)).contiguous()
+
+
+@pytest.mark.parametrize("dims", [128, 64])
+@pytest.mark.parametrize("k", [1, 32, 100, 256])
+def test_assign_lockstep_fp32(announce, dims, k):
+    g = _gen(k + dims)
+    x = _mixture(g, 2, 2048, dims, 16)
+    c = _centres_with_duplicates(g, x, k) if k > 1 else x[:, :1].contiguous()
+    announce(f"D={dims} K={k}")
+    labels = torch.empty(2, 2048, dtype=torch.int32, device=DEV)
+    norms = torch.empty(2, k, device=DEV)
+    clustering_cuda.assign_tokens_to_centers(x.to(DEV), c.to(DEV), labels, torch.empty(1, device=DEV), norms, 1024)
+    ref_norms = canonical.center_norms(c.numpy())
+    ref = canonical.assign(x.numpy(), c.numpy(), ref_norms)
+    assert np.array_equal(norms.cpu().numpy().view(np.int32), ref_norms.view(np.int32))
+    assert np.array_equal(labels.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("dims", [128, 64])
+def test_update_lockstep_fp32(announce, dims):
+    g = _gen(dims + 5)
+    x = _mixture(g, 3, 3000, dims, 10)
+    k = 40
+    labels = torch.randint(k - 3, (3, 3000), generator=g, dtype=torch.int32)  # last 3 clusters empty
+    prev = torch.randn(3, k, dims, generator=g)
+    announce(f"D={dims}")
+    sums = torch.empty(3, k, dims, device=DEV)
+    counts = torch.empty(3, k, dtype=torch.int32, device=DEV)
+    means = torch.empty(3, k, dims, device=DEV)
+    clustering_cuda.recompute_cluster_centers(x.to(DEV), labels.to(DEV), prev.to(DEV), sums, counts, means)
+    rs, rc, rm = canonical.update(x.numpy(), labels.numpy(), prev.numpy())
+    assert np.array_equal(counts.cpu().numpy(), rc)
+    assert np.array_equal(sums.cpu().numpy().view(np.int32), rs.view(np.int32))
+    assert np.array_equal(means.cpu().numpy().view(np.int32), rm.view(np.int32))
+
+
+@pytest.mark.parametrize("dtype,dims,n,kq,kk,iters", [
+    (torch.float32, 128, 2048, 32, 32, 10),
+    (torch.bfloat16, 128, 6750, 64, 256, 10),
+    (torch.float16, 64, 3000, 20, 50, 6),
+])
+def test_fused_fit_bit_exact(announce, dtype, dims, n, kq, kk, iters):
+    g = _gen(n + kq)
+    bh = 2
+    q = _mixture(g, bh, n, dims, 32, 1.5).to(dtype)
+    k = _mixture(g, bh, n, dims, 64, 1.5).to(dtype)
+    qi = _centres_with_duplicates(g, q, kq)
+    ki = _centres_with_duplicates(g, k, kk)
+    announce(f"{dtype} D={dims} N={n} KQ={kq} KK={kk} iters={iters}")
+    (ql, qc, qn, qidx, qoff), (kl, kc, kn, kidx, koff) = clustering_cuda.kmeans_fit(
+        [clustering_cuda.KMeansProblem(q.to(DEV), qi.to(DEV)), clustering_cuda.KMeansProblem(k.to(DEV), ki.to(DEV))],
+        iters)
+    for (lab, cen, cnt, idx, off), x, init in (((ql, qc, qn, qidx, qoff), q, qi), ((kl, kc, kn, kidx, koff), k, ki)):
+        rl, rc, rn, ridx, roff = canonical.kmeans_fit(x.float().numpy(), init.numpy(), iters)
+        assert np.array_equal(lab.cpu().numpy(), rl)
+        assert np.array_equal(cnt.cpu().numpy(), rn)
+        assert np.array_equal(cen.cpu().numpy().view(np.int32), rc.view(np.int32))
+        assert np.array_equal(idx.cpu().numpy(), ridx)
+        assert np.array_equal(off.cpu().numpy(), roff)
+
+
+def test_fit_token_clusters_api(announce):
+    g = _gen(77)
+    x = _mixture(g, 2, 1000, 128, 8).to(torch.bfloat16)
+    init = _centres_with_duplicates(g, x, 16)
+    announce()
+    labels, centers, counts, it = clustering.fit_token_clusters(x.to(DEV), 16, max_iters=5, tol=0,
+                                                                 init_centroids=init.to(DEV))
+    rl, rc, rn, _, _ = canonical.kmeans_fit(x.float().numpy(), init.numpy(), 5)
+    assert it == 5
+    assert np.array_equal(labels.cpu().numpy(), rl)
+    assert np.array_equal(centers.cpu().numpy().view(np.int32), rc.view(np.int32))
+    # tol>0: stops once the centres stop moving; result is still a fixed point of the oracle.
+    labels2, centers2, counts2, it2 = clustering.fit_token_clusters(x.to(DEV), 16, max_iters=100, tol=1e-6,
+                                                                    init_centroids=init.to(DEV))
+    rl2, rc2, _, _, _ = canonical.kmeans_fit(x.float().numpy(), init.numpy(), it2)
+    assert np.array_equal(labels2.cpu().numpy(), rl2)
+    assert np.array_equal(centers2.cpu().numpy().view(np.int32), rc2.view(np.int32))
+
+
+# ---------------------------------------------------------------- stage 4: sparse attention
+
+def _random_partition(g, n, c, empty=0):
+    cuts = torch.sort(torch.randint(n + 1, (c - 1,), generator=g)).values
+    sizes = torch.diff(torch.cat([torch.tensor([0]), cuts, torch.tensor([n])]))
+    if empty:
+        sizes[:empty] = 0
+        sizes[-1] += n - sizes.sum()
+    return sizes.to(torch.int32)
+
+
+def _check_attention(out, ref):
+    err = (out.float().cpu() - torch.from_numpy(ref)).abs()
+    assert err.max().item() <= 2e-2, f"max abs error {err.max().item():.3e}"
+    assert err.mean().item() <= 2e-3, f"mean abs error {err.mean().item():.3e}"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dims", [128, 64])
+@pytest.mark.parametrize("density", [0.3, 1.0])
+def test_sparse_attention_matches_oracle(announce, dtype, dims, density):
+    g = _gen(int(density * 10) + dims)
+    h, sq, sk, cq, ck = 3, 1100, 1300, 9, 23
+    q = torch.randn(1, h, sq, dims, generator=g).to(dtype)
+    k = torch.randn(1, h, sk, dims, generator=g).to(dtype)
+    v = torch.randn(1, h, sk, dims, generator=g).to(dtype)
+    qs = torch.stack([_random_partition(g, sq, cq, empty=1) for _ in range(h)])[None]
+    ks = torch.stack([_random_partition(g, sk, ck, empty=2) for _ in range(h)])[None]
+    m = torch.rand(1, h, cq, ck, generator=g) < density
+    m[0, 0, 2] = False  # one fully masked query cluster -> zero rows
+    announce(f"{dtype} D={dims} density={density}")
+    out = attention_cuda.sparse_attention(q.to(DEV), k.to(DEV), v.to(DEV), m.to(DEV), qs.to(DEV), ks.to(DEV))
+    ref = canonical.sparse_attention(q[0].float().numpy(), k[0].float().numpy(), v[0].float().numpy(),
+                                     m[0].numpy(), qs[0].numpy(), ks[0].numpy())
+    _check_attention(out[0], ref)
+    off = int(qs[0, 0, :2].sum())
+    rows = int(qs[0, 0, 2])
+    assert torch.all(out[0, 0, off:off + rows].float() == 0)
+
+
+def test_sparse_attention_dense_equals_sdpa(announce):
+    g = _gen(5)
+    q = torch.randn(1, 2, 700, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(1, 2, 900, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(1, 2, 900, 128, generator=g).to(torch.bfloat16)
+    qs = torch.tensor([[[300, 400], [700, 0]]], dtype=torch.int32)
+    ks = torch.tensor([[[500, 400], [100, 800]]], dtype=torch.int32)
+    m = torch.ones(1, 2, 2, 2, dtype=torch.bool)
+    announce()
+    out = attention_cuda.sparse_attention(q.to(DEV), k.to(DEV), v.to(DEV), m.to(DEV), qs.to(DEV), ks.to(DEV))
+    ref = torch.nn.functional.scaled_dot_product_attention(q.double(), k.double(), v.double())
+    err = (out.cpu().double() - ref).abs()
+    assert err.max().item() <= 2e-2 and err.mean().item() <= 2e-3
+
+
+def test_sparse_attention_out_index_scatter(announce):
+    g = _gen(9)
+    h, s, d = 2, 600, 128
+    q = torch.randn(1, h, s, d, generator=g).to(torch.bfloat16)
+    k = torch.randn(1, h, s, d, generator=g).to(torch.bfloat16)
+    v = torch.randn(1, h, s, d, generator=g).to(torch.bfloat16)
+    qs = torch.tensor([[[200, 400], [100, 500]]], dtype=torch.int32)
+    ks = torch.tensor([[[300, 300], [350, 250]]], dtype=torch.int32)
+    m = torch.tensor([[[[True, False], [True, True]], [[False, True], [True, False]]]])
+    perm = torch.stack([torch.randperm(s, generator=g) for _ in range(h)]).to(torch.int32)
+    announce()
+    args = [t.to(DEV) for t in (q, k, v, m, qs, ks)]
+    plain = attention_cuda.sparse_attention(*args)
+    fused = attention_cuda.sparse_attention(*args, out_index=perm.to(DEV))
+    restored = clustering.restore_sequence_order(plain, perm.to(DEV))
+    assert torch.equal(fused.cpu().view(torch.int16), restored.cpu().view(torch.int16))
