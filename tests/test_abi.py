@@ -1,0 +1,52 @@
+"""The C-ABI library loads without a GPU and exports every symbol include/peco_hip.h declares."""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+from peco_amd import _native
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "peco_hip.h"
+
+
+def _declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(peco_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_reference_symbols():
+    names = _declared()
+    for ref in ("peco_assign_tokens_to_centers", "peco_recompute_cluster_centers", "peco_reorder_token_features",
+                "peco_cluster_error_message", "peco_sparse_attention", "peco_attention_error_string"):
+        assert ref in names
+
+
+def test_library_exports_every_declared_symbol():
+    if not _native.LIB_PATH.exists():
+        _native.build_library()
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_native.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r" T (peco_\w+)", out))
+    missing = [n for n in _declared() if n not in exported]
+    assert not missing, f"declared but not exported: {missing}"
+    assert set(_native.SIGNATURES) == set(_declared())
+
+
+def test_library_loads_and_reports_status_strings_without_a_gpu():
+    lib = _native.library()
+    assert lib.peco_abi_version() == 1
+    assert b"workspace" in lib.peco_cluster_error_message(20001)
+    assert lib.peco_attention_error_string(0)
+    # Size queries are host-only arithmetic.
+    assert lib.peco_sparse_attention_workspace_size(24, 7006, 7006, 66, 258) <= 24 * (258 + 2 + 3 * (438 + 66))
+    assert lib.peco_kmeans_workspace_size(24, 6750, 256, 128) > 0
+    assert lib.peco_cluster_sort_workspace_size(24, 6750, 256) > 0
+
+
+def test_invalid_arguments_are_rejected_before_any_launch():
+    lib = _native.library()
+    null = ctypes.c_void_p(0)
+    assert lib.peco_reorder_token_features(null, null, null, 1, 4, 8, 3, 0, null) == 1
+    assert lib.peco_sparse_attention(null, null, null, null, null, null, null, null, 1, 4, 4, 96, 1, 1, 1,
+                                     null) == 1
+    assert lib.peco_cluster_sort(null, 1, 4, 2, null, null, null, null, null, 0, null) == 1
