@@ -209,21 +209,77 @@ template <> struct Mfma<kBF16> {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                        0, 0, 0);
     }
+    // Two fp32 -> packed pair with round-to-nearest-even (v_cvt_pk_bf16_f32).
+    static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+        typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+        typedef float f2 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, b2));
+    }
 };
 template <> struct Mfma<kF16> {
     static __device__ __forceinline__ f32x16 run(u16x8 a, u16x8 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
                                                       0, 0, 0);
     }
+    static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        typedef float f2 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, h2));
+    }
 };
 
-// LDS strides (in 16-bit elements): K tile rows of D channels (+8 pad), V^T rows of 64 keys (+4 pad).
+// K and V tiles live in LDS row-major ([64 keys][D], no padding) and are filled straight
+// from global memory with 16-byte global_load_lds, which writes each wave's 64 lanes to one
+// contiguous 1 KB span. Bank conflicts are avoided by XOR-swizzling the 16-byte chunks of a
+// row: a lane whose LDS slot is (row, physical chunk p) fetches logical chunk p ^ swz(row).
+//   K: swz = row % CH, so the 16 rows read by one S^T A-fragment quarter-wave hit 16 chunks.
+//   V: swz spreads the 4 rows x 32 bytes of one transpose read over distinct banks.
 template <int D> struct Tiles {
-    static constexpr int kRow = D + 8;
-    static constexpr int vRow = kKTile + 4;
-    static constexpr int kElems = kKTile * kRow;
-    static constexpr int vElems = D * vRow;
+    static constexpr int CH = D / 8;                  // 16-byte chunks per row
+    static constexpr int kElems = kKTile * D;
+    static constexpr int kWaveRows = kWave / CH;      // rows per wave-wide direct load
+    static constexpr int kLoads = kKTile / (4 * kWaveRows);  // direct loads per wave per tile
+    static __device__ __forceinline__ int swz_k(int row) { return row % CH; }
+    static __device__ __forceinline__ int swz_v(int row) { return CH == 16 ? 4 * (row % 4) : 4 * ((row >> 1) & 1); }
 };
+
+// Physical key row of virtual stream row r: the largest cluster c with soff[c] <= r holds it.
+__device__ __forceinline__ int stream_row(const int* soff, const int* kpre, int ck, int r) {
+    int lo = 0, hi = ck - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (soff[mid] <= r) lo = mid;
+        else hi = mid - 1;
+    }
+    return kpre[lo] + (r - soff[lo]);
+}
+
+// Issue the direct-to-LDS loads of one K and one V tile (no wait). Rows past the stream end
+// read row 0 of the head: their K scores are masked to -inf and their P is 0.
+template <int D>
+__device__ __forceinline__ void load_tile_lds(uint16_t* ks, uint16_t* vs, const uint16_t* kh, const uint16_t* vh,
+                                              const int* prow, int wave, int lane) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    using T = Tiles<D>;
+    int rows[T::kLoads];
+#pragma unroll
+    for (int i = 0; i < T::kLoads; ++i) rows[i] = prow[(i * 4 + wave) * T::kWaveRows + lane / T::CH];
+#pragma unroll
+    for (int i = 0; i < T::kLoads; ++i) {
+        const int r = (i * 4 + wave) * T::kWaveRows + lane / T::CH;  // tile row written by this lane
+        const int p = lane % T::CH;                                      // physical chunk
+        const int64_t g = static_cast<int64_t>(rows[i]) * D;
+        uint16_t* kdst = ks + (i * 4 + wave) * kWave * 8;
+        uint16_t* vdst = vs + (i * 4 + wave) * kWave * 8;
+        __builtin_amdgcn_global_load_lds(kh + g + (p ^ T::swz_k(r)) * 8,
+                                         (__attribute__((address_space(3))) void*)kdst, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vh + g + (p ^ T::swz_v(r)) * 8,
+                                         (__attribute__((address_space(3))) void*)vdst, 16, 0, 0);
+    }
+#endif
+}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 template <int DT, int D>
 __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
@@ -233,9 +289,11 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     using T = Tiles<D>;
     constexpr int S = D / 16;       // k-steps of S^T over channels
     constexpr int NB = D / 32;      // 32-channel blocks of O^T
-    __shared__ uint16_t ks[T::kElems];
-    __shared__ uint16_t vt[T::vElems];
-    __shared__ int prow[kKTile];
+    // Scores may run up to 2^8 above the running maximum before O is rescaled.
+    constexpr float kLazyLog2 = 8.0f;
+    __shared__ __align__(16) uint16_t ks[2][T::kElems];
+    __shared__ __align__(16) uint16_t vs[2][T::kElems];
+    __shared__ int prow[2][kKTile];
     __shared__ int tmp[4];
     extern __shared__ int dyn[];
     int* soff = dyn;            // [ck] stream offset of each key cluster
@@ -249,7 +307,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     const int q_start = item[0], qc = item[1], q_rows = item[2];
     const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave, h = lane / 32;
 
-    // Key stream of this query cluster.
+    // Key stream of this query cluster: kept clusters in order, offsets soff.
     const uint8_t* sel = selected + (static_cast<int64_t>(bh) * cq + qc) * ck;
     const int32_t* gk = W.kprefix + static_cast<int64_t>(bh) * (ck + 1);
     int L;
@@ -269,6 +327,13 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
             run += sel[c] ? gk[c + 1] - gk[c] : 0;
         }
     }
+    __syncthreads();
+    const int ntiles = static_cast<int>(ceil_div(L, kKTile));
+    if (tid < kKTile) {
+        prow[0][tid] = tid < L ? stream_row(soff, kpre, ck, tid) : 0;
+        const int r1 = kKTile + tid;
+        prow[1][tid] = r1 < L ? stream_row(soff, kpre, ck, r1) : 0;
+    }
 
     // Q^T operand: lane holds query row (32*wave + l%32), channels 16s + 8h .. +7.
     const int qrow = wave * 32 + (lane % 32);
@@ -284,123 +349,105 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     f32x16 oacc[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) oacc[nb] = f32x16{};
-    float m_run = -INFINITY, l_run = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f, neg_m = 0.0f;
+    const float lazy = kLazyLog2 / scale_log2;
 
     const uint16_t* kh = k + head * sk * D;
     const uint16_t* vh = v + head * sk * D;
-    const int ntiles = static_cast<int>(ceil_div(L, kKTile));
+    // Per-lane constants of the fragment reads.
+    const int arow = lane % 32;                 // S^T A row (key within a 32-key block)
+    const int gsub = (lane / 16) % 2;           // 16-lane group parity (V^T channel half)
+    const int src = lane % 16;                  // source lane of the transpose read
+    __syncthreads();
+    if (ntiles > 0) load_tile_lds<D>(ks[0], vs[0], kh, vh, prow[0], wave, lane);
+    __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0): this wave's tile-0 loads have landed
+    __syncthreads();
     for (int tile = 0; tile < ntiles; ++tile) {
-        const int base = tile * kKTile;
-        __syncthreads();  // previous tile fully consumed; soff/kpre visible
-        if (tid < kKTile) {
-            const int r = base + tid;
-            int phys = -1;
-            if (r < L) {
-                // Largest cluster c with soff[c] <= r (it is non-empty and holds r).
-                int lo = 0, hi = ck - 1;
-                while (lo < hi) {
-                    const int mid = (lo + hi + 1) >> 1;
-                    if (soff[mid] <= r) lo = mid;
-                    else hi = mid - 1;
+        const int buf = tile & 1;
+        const bool more = tile + 1 < ntiles;
+        if (more) load_tile_lds<D>(ks[buf ^ 1], vs[buf ^ 1], kh, vh, prow[buf ^ 1], wave, lane);
+        if (wave_active) {
+            const int base = tile * kKTile;
+            const bool partial = base + kKTile > L;
+            const uint16_t* kt = ks[buf];
+            const uint16_t* vt = vs[buf];
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
+                f32x16 sacc = {};
+                const int krow = 32 * cb + arow;
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    const int pc = (2 * s + h) ^ T::swz_k(krow);
+                    const u16x8 kf = *reinterpret_cast<const u16x8*>(kt + krow * D + pc * 8);
+                    sacc = Mfma<DT>::run(kf, qf[s], sacc);
                 }
-                phys = kpre[lo] + (r - soff[lo]);
+                if (partial) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int key = base + 32 * cb + 8 * (i / 4) + 4 * h + (i % 4);
+                        if (key >= L) sacc[i] = -INFINITY;
+                    }
+                }
+                float tmax = sacc[0];
+#pragma unroll
+                for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, sacc[i]);
+                tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+                if (__any(tmax > m_run + lazy)) {
+                    const float m_new = fmaxf(m_run, tmax);
+                    const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
+                    m_run = m_new;
+                    neg_m = -m_new * scale_log2;
+                    l_run *= alpha;
+#pragma unroll
+                    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) oacc[nb][i] *= alpha;
+                }
+                float psum = 0.0f;
+                uint32_t pp[8];
+#pragma unroll
+                for (int i = 0; i < 16; i += 2) {
+                    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[i], scale_log2, neg_m));
+                    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[i + 1], scale_log2, neg_m));
+                    psum += p0;
+                    psum += p1;
+                    pp[i / 2] = Mfma<DT>::pack2(p0, p1);
+                }
+                l_run += psum;
+                // O^T += V^T P^T over the two 16-key k-steps of this 32-key half. The V^T
+                // fragment (channel 32nb + l%32, 8 keys) comes from two transpose reads: source
+                // lane r of each 16-lane group points at key 32cb+16kk+8t+4h+r/4, channels
+                // 32nb + 16*gsub + 4*(r%4) .. +3.
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    const u16x8 pf = __builtin_bit_cast(u16x8, u32x4{pp[4 * kk], pp[4 * kk + 1], pp[4 * kk + 2],
+                                                                    pp[4 * kk + 3]});
+#pragma unroll
+                    for (int nb = 0; nb < NB; ++nb) {
+                        s16x4 part[2];
+#pragma unroll
+                        for (int t = 0; t < 2; ++t) {
+                            const int vrow = 32 * cb + 16 * kk + 8 * t + 4 * h + src / 4;
+                            const int d = 32 * nb + 16 * gsub + 4 * (src % 4);
+                            const int pc = (d / 8) ^ T::swz_v(vrow);
+                            const uint16_t* a = vt + vrow * D + pc * 8 + (d % 8);
+                            part[t] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                (__attribute__((address_space(3))) s16x4*)(a));
+                        }
+                        const u16x8 af = __builtin_bit_cast(
+                            u16x8, u32x4{__builtin_bit_cast(u32x2, part[0])[0], __builtin_bit_cast(u32x2, part[0])[1],
+                                         __builtin_bit_cast(u32x2, part[1])[0], __builtin_bit_cast(u32x2, part[1])[1]});
+                        oacc[nb] = Mfma<DT>::run(af, pf, oacc[nb]);
+                    }
+                }
             }
-            prow[tid] = phys;
         }
+        if (more && tid < kKTile) {
+            const int r = (tile + 2) * kKTile + tid;
+            prow[buf][tid] = r < L ? stream_row(soff, kpre, ck, r) : 0;
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of the next tile have landed
         __syncthreads();
-        // K tile: row-major [key][D] (+pad). 16 lanes per key row, 16 bytes each.
-        {
-            constexpr int CH = D / 8;          // 16-byte chunks per row
-            constexpr int RPP = 256 / CH;      // rows per pass
-#pragma unroll
-            for (int pass = 0; pass < kKTile / RPP; ++pass) {
-                const int kr = pass * RPP + tid / CH;
-                const int ch = tid % CH;
-                const int pr = prow[kr];
-                u32x4 val = u32x4{0, 0, 0, 0};
-                if (pr >= 0) val = *reinterpret_cast<const u32x4*>(kh + static_cast<int64_t>(pr) * D + ch * 8);
-                *reinterpret_cast<u32x4*>(ks + kr * T::kRow + ch * 8) = val;
-            }
-        }
-        // V^T tile: [D][64 keys] (+pad). Thread: 4 consecutive keys x 8 channels.
-        {
-            constexpr int DC = D / 8;
-            for (int id = tid; id < 16 * DC; id += 256) {
-                const int kq = id % 16, dc = id / 16;
-                u16x8 rows[4];
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int pr = prow[4 * kq + r];
-                    rows[r] = pr >= 0 ? *reinterpret_cast<const u16x8*>(vh + static_cast<int64_t>(pr) * D + dc * 8)
-                                      : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-                }
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const uint32_t lo = rows[0][i] | (static_cast<uint32_t>(rows[1][i]) << 16);
-                    const uint32_t hi = rows[2][i] | (static_cast<uint32_t>(rows[3][i]) << 16);
-                    *reinterpret_cast<u32x2*>(vt + (dc * 8 + i) * T::vRow + 4 * kq) = u32x2{lo, hi};
-                }
-            }
-        }
-        __syncthreads();
-        if (!wave_active) continue;
-
-        // S^T for two 32-key blocks.
-        f32x16 sacc[2];
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-            f32x16 acc = {};
-#pragma unroll
-            for (int s = 0; s < S; ++s) {
-                const u16x8 kf = *reinterpret_cast<const u16x8*>(ks + (32 * cb + lane % 32) * T::kRow + 16 * s + 8 * h);
-                acc = Mfma<DT>::run(kf, qf[s], acc);
-            }
-            sacc[cb] = acc;
-        }
-        // Online softmax (per query l%32; the two lane halves hold disjoint keys).
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int key = base + 32 * cb + 8 * (i / 4) + 4 * h + (i % 4);
-                const float sv = key < L ? sacc[cb][i] * scale_log2 : -INFINITY;
-                sacc[cb][i] = sv;
-                tmax = fmaxf(tmax, sv);
-            }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
-        const float m_new = fmaxf(m_run, tmax);
-        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-        m_run = m_new;
-        float psum = 0.0f;
-        u16x8 pf[4];  // P^T operands for the four 16-key k-steps
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float pv = __builtin_amdgcn_exp2f(sacc[cb][i] - m_use);
-                psum += pv;
-                // k-step ks = 2*cb + (i/8); element j = i % 8 (keys 8g+4h+r, g = i/4).
-                pf[2 * cb + i / 8][i % 8] = f32_to_half<DT>(pv);
-            }
-        l_run = l_run * alpha + psum;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) oacc[nb][i] *= alpha;
-        // O^T += V^T P^T.
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            const uint16_t* vrow = vt + (32 * nb + lane % 32) * T::vRow;
-#pragma unroll
-            for (int kstep = 0; kstep < 4; ++kstep) {
-                const u32x2 a0 = *reinterpret_cast<const u32x2*>(vrow + 16 * kstep + 4 * h);
-                const u32x2 a1 = *reinterpret_cast<const u32x2*>(vrow + 16 * kstep + 8 + 4 * h);
-                const u32x4 af = u32x4{a0[0], a0[1], a1[0], a1[1]};
-                oacc[nb] = Mfma<DT>::run(__builtin_bit_cast(u16x8, af), pf[kstep], oacc[nb]);
-            }
-        }
     }
     if (!qvalid) return;
     const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
@@ -413,10 +460,8 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int d0 = 32 * nb + 8 * g + 4 * h;
-            const uint32_t w0 = f32_to_half<DT>(oacc[nb][4 * g + 0] * inv) |
-                                (static_cast<uint32_t>(f32_to_half<DT>(oacc[nb][4 * g + 1] * inv)) << 16);
-            const uint32_t w1 = f32_to_half<DT>(oacc[nb][4 * g + 2] * inv) |
-                                (static_cast<uint32_t>(f32_to_half<DT>(oacc[nb][4 * g + 3] * inv)) << 16);
+            const uint32_t w0 = Mfma<DT>::pack2(oacc[nb][4 * g + 0] * inv, oacc[nb][4 * g + 1] * inv);
+            const uint32_t w1 = Mfma<DT>::pack2(oacc[nb][4 * g + 2] * inv, oacc[nb][4 * g + 3] * inv);
             *reinterpret_cast<u32x2*>(o + d0) = u32x2{w0, w1};
         }
 }

@@ -47,13 +47,13 @@ struct KmProblem {
     int32_t* tile_hist;     // [batch, sort tiles, K]
     float* sums;            // nullable [batch, K, D]: per-cluster sums of the last update
     int batch, tokens, clusters;
-    int assign_begin;       // first linear assign block (batch * ceil(tokens/128) blocks)
+    int assign_begin;       // first linear assign block (batch * ceil(tokens/256) blocks)
     int update_begin;       // first linear update block (batch * K blocks)
     int sort_tiles;
 };
 
 constexpr int kMaxKm = 2;
-constexpr int kAssignTile = 128;  // tokens per assign workgroup (4 waves x 32 tokens)
+constexpr int kAssignTile = 256;  // tokens per assign workgroup (4 waves x 64 tokens)
 
 struct KmArgs {
     KmProblem p[kMaxKm];
@@ -162,13 +162,59 @@ __device__ __forceinline__ void load_x8(const void* x, int64_t e, bool valid, u1
     }
 }
 
-// Assign: one workgroup = 128 tokens of one (problem, batch); wave w owns tokens
-// [32w, 32w+32). MFMA 32x32x16: A = centres (32 rows x 16 channels), B = tokens
-// (16 channels x 32 tokens); lane l holds token l%32 and centres 8*(i/4)+4*(l/32)+i%4.
+// Assign: one workgroup = 256 tokens of one (problem, batch); wave w owns tokens
+// [64w, 64w+64) as two 32-token MFMA column blocks. Centres stream through LDS in blocks of
+// 32 (split-bf16 hi/lo rows + canonical norms), double-buffered with a register prefetch.
+// MFMA 32x32x16: A = centres (32 rows x 16 channels), B = tokens (16 channels x 32 tokens);
+// lane l holds token l%32 of each column block and centres 8*(i/4)+4*(l/32)+i%4.
+template <int D> struct AssignTiles {
+    static constexpr int kRow = D + 8;                 // padded LDS row (16-bit elements)
+    static constexpr int kElems = 32 * kRow;
+    static constexpr int kChunks = D / 8;              // 16-byte chunks per row
+    static constexpr int kLoads = 32 * kChunks / 256;  // 16-byte loads per thread per array
+};
+
+template <int D> struct CentreRegs {
+    u32x4 hi[AssignTiles<D>::kLoads], lo[AssignTiles<D>::kLoads];
+    float norm;
+};
+
+template <int D>
+__device__ __forceinline__ void load_centres(CentreRegs<D>& R, const uint16_t* hi_base, const uint16_t* lo_base,
+                                             const float* norms, int cb, int K, int tid) {
+    using T = AssignTiles<D>;
+#pragma unroll
+    for (int i = 0; i < T::kLoads; ++i) {
+        const int id = i * 256 + tid;
+        const int row = min(cb + id / T::kChunks, K - 1);  // rows past K are never selected
+        const int64_t e = static_cast<int64_t>(row) * D + (id % T::kChunks) * 8;
+        R.hi[i] = *reinterpret_cast<const u32x4*>(hi_base + e);
+        R.lo[i] = *reinterpret_cast<const u32x4*>(lo_base + e);
+    }
+    if (tid < 32) R.norm = cb + tid < K ? norms[cb + tid] : INFINITY;
+}
+
+template <int D>
+__device__ __forceinline__ void store_centres(const CentreRegs<D>& R, uint16_t* hi, uint16_t* lo, float* nrm, int tid) {
+    using T = AssignTiles<D>;
+#pragma unroll
+    for (int i = 0; i < T::kLoads; ++i) {
+        const int id = i * 256 + tid;
+        const int off = (id / T::kChunks) * T::kRow + (id % T::kChunks) * 8;
+        *reinterpret_cast<u32x4*>(hi + off) = R.hi[i];
+        *reinterpret_cast<u32x4*>(lo + off) = R.lo[i];
+    }
+    if (tid < 32) nrm[tid] = R.norm;
+}
+
 template <int DT, int D>
-__global__ __launch_bounds__(256) void km_assign_kernel(KmArgs a, KmIter it) {
+__global__ __launch_bounds__(256, 2) void km_assign_kernel(KmArgs a, KmIter it) {
+    using T = AssignTiles<D>;
     constexpr int S = D / 16;                 // MFMA k-steps over channels
     constexpr bool kSplitX = DT != kBF16;
+    __shared__ uint16_t chi[2][T::kElems];
+    __shared__ uint16_t clo[2][T::kElems];
+    __shared__ float cn[2][32];
     __shared__ float red[4];
     const int p = km_problem(a, blockIdx.x, true);
     const KmProblem& P = a.p[p];
@@ -177,119 +223,143 @@ __global__ __launch_bounds__(256) void km_assign_kernel(KmArgs a, KmIter it) {
     const int b = local / tiles_per_batch;
     const int tile = local % tiles_per_batch;
     const int K = P.clusters;
-    const int lane = threadIdx.x % kWave;
-    const int wave = threadIdx.x / kWave;
+    const int tid = threadIdx.x;
+    const int lane = tid % kWave;
+    const int wave = tid / kWave;
     const int h = lane / 32;
-    const int t = tile * kAssignTile + wave * 32 + (lane % 32);
-    const bool valid = t < P.tokens;
-    const int64_t row = static_cast<int64_t>(b) * P.tokens + t;
-    const int64_t xrow = static_cast<int64_t>(b) * P.x_stride + static_cast<int64_t>(t) * D;
     const float* norms = P.norms + static_cast<int64_t>(b) * K;
+    const uint16_t* hi_base = P.prep_hi + static_cast<int64_t>(b) * K * D;
+    const uint16_t* lo_base = P.prep_lo + static_cast<int64_t>(b) * K * D;
+
+    CentreRegs<D> regs;
+    load_centres<D>(regs, hi_base, lo_base, norms, 0, K, tid);
 
     // Largest centre norm of this batch entry (for the error bound).
     float nmax = 0.0f;
-    for (int j = threadIdx.x; j < K; j += blockDim.x) nmax = fmaxf(nmax, norms[j]);
+    for (int j = tid; j < K; j += blockDim.x) nmax = fmaxf(nmax, norms[j]);
 #pragma unroll
     for (int m = 1; m < kWave; m <<= 1) nmax = fmaxf(nmax, __shfl_xor(nmax, m, kWave));
     if (lane == 0) red[wave] = nmax;
+
+    int tok[2];
+    bool valid[2];
+    u16x8 xh[2][S], xl[2][S];
+    float sq[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        tok[c] = tile * kAssignTile + wave * 64 + 32 * c + (lane % 32);
+        valid[c] = tok[c] < P.tokens;
+        const int64_t xrow = static_cast<int64_t>(b) * P.x_stride + static_cast<int64_t>(tok[c]) * D;
+#pragma unroll
+        for (int s = 0; s < S; ++s) load_x8<DT>(P.x, xrow + 16 * s + 8 * h, valid[c], xh[c][s], xl[c][s], sq[c]);
+        sq[c] += __shfl_xor(sq[c], 32, kWave);
+    }
+    store_centres<D>(regs, chi[0], clo[0], cn[0], tid);
     __syncthreads();
     nmax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 
-    u16x8 xh[S], xl[S];
-    float sq = 0.0f;
-#pragma unroll
-    for (int s = 0; s < S; ++s) load_x8<DT>(P.x, xrow + 16 * s + 8 * h, valid, xh[s], xl[s], sq);
-    sq += __shfl_xor(sq, 32, kWave);
-
-    float m1 = INFINITY, m2 = INFINITY;
-    int id1 = 0;
-    const uint16_t* hi_base = P.prep_hi + static_cast<int64_t>(b) * K * D;
-    const uint16_t* lo_base = P.prep_lo + static_cast<int64_t>(b) * K * D;
-    for (int cb = 0; cb < K; cb += 32) {
-        const int crow = cb + (lane % 32);
-        const bool cvalid = crow < K;
-        f32x16 acc = {};
+    float m1[2] = {INFINITY, INFINITY}, m2[2] = {INFINITY, INFINITY};
+    int id1[2] = {0, 0};
+    const int nblocks = static_cast<int>(ceil_div(K, 32));
+    for (int blk = 0; blk < nblocks; ++blk) {
+        const int buf = blk & 1;
+        const bool more = blk + 1 < nblocks;
+        if (more) load_centres<D>(regs, hi_base, lo_base, norms, (blk + 1) * 32, K, tid);
+        f32x16 acc[2] = {f32x16{}, f32x16{}};
+        const uint16_t* hrow = chi[buf] + (lane % 32) * T::kRow + 8 * h;
+        const uint16_t* lrow = clo[buf] + (lane % 32) * T::kRow + 8 * h;
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-            u16x8 ah = u16x8{0, 0, 0, 0, 0, 0, 0, 0}, al = ah;
-            if (cvalid) {
-                ah = *reinterpret_cast<const u16x8*>(hi_base + static_cast<int64_t>(crow) * D + 16 * s + 8 * h);
-                al = *reinterpret_cast<const u16x8*>(lo_base + static_cast<int64_t>(crow) * D + 16 * s + 8 * h);
+            const bf16x8 ah = as_bf16x8(*reinterpret_cast<const u16x8*>(hrow + 16 * s));
+            const bf16x8 al = as_bf16x8(*reinterpret_cast<const u16x8*>(lrow + 16 * s));
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, as_bf16x8(xh[c][s]), acc[c], 0, 0, 0);
+                acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, as_bf16x8(xh[c][s]), acc[c], 0, 0, 0);
+                if constexpr (kSplitX)
+                    acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, as_bf16x8(xl[c][s]), acc[c], 0, 0, 0);
             }
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(ah), as_bf16x8(xh[s]), acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(al), as_bf16x8(xh[s]), acc, 0, 0, 0);
-            if constexpr (kSplitX)
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(ah), as_bf16x8(xl[s]), acc, 0, 0, 0);
         }
+        const int cb = blk * 32;
+        float nv[16];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
+            const f32x4 n4 = *reinterpret_cast<const f32x4*>(&cn[buf][8 * g + 4 * h]);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int j = cb + 8 * g + 4 * h + r;
-                const float v = j < K ? acc[4 * g + r] + norms[j] : INFINITY;
-                const float nm2 = fminf(m2, fmaxf(m1, v));
-                id1 = v < m1 ? j : id1;
-                m1 = fminf(m1, v);
-                m2 = nm2;
+            for (int r = 0; r < 4; ++r) nv[4 * g + r] = n4[r];
+        }
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int j = cb + 8 * (i / 4) + 4 * h + (i % 4);
+                const float v = acc[c][i] + nv[i];  // +inf for centres past K
+                const float nm2 = fminf(m2[c], fmaxf(m1[c], v));
+                id1[c] = v < m1[c] ? j : id1[c];
+                m1[c] = fminf(m1[c], v);
+                m2[c] = nm2;
             }
         }
+        if (more) store_centres<D>(regs, chi[buf ^ 1], clo[buf ^ 1], cn[buf ^ 1], tid);
+        __syncthreads();
     }
-    // Merge the two lane halves that hold the same token.
-    {
-        const float pm1 = __shfl_xor(m1, 32, kWave);
-        const float pm2 = __shfl_xor(m2, 32, kWave);
-        const int pid = __shfl_xor(id1, 32, kWave);
-        const float nm2 = fminf(fminf(m2, pm2), fmaxf(m1, pm1));
-        if (pm1 < m1 || (pm1 == m1 && pid < id1)) {
-            m1 = pm1;
-            id1 = pid;
-        }
-        m2 = nm2;
-    }
-    // Certified decision: gap > 2E proves id1 is the canonical argmin.
-    const float xnorm = sqrtf(sq) * 1.001f;
-    const float cmax = sqrtf(nmax) * 1.001f;
-    const float thr = 1.05f * (2.0f * a.kappa * xnorm * cmax) + 4.0f * 5.9604645e-8f * (fabsf(m1) + fabsf(m2)) + 1e-30f;
-    const bool sure = (m2 - m1) > thr;
-    int label = id1;
-    const bool flagged = valid && !sure;
 
-    // Canonical re-evaluation of flagged tokens, one token at a time per wave.
-    uint64_t pending = __ballot(flagged && h == 0);
+    const float cmax = sqrtf(nmax) * 1.001f;
     const float* cent = it.src[p] + static_cast<int64_t>(b) * K * D;
-    while (pending) {
-        const int src_lane = __builtin_ctzll(pending);
-        pending &= pending - 1;
-        const int tok = tile * kAssignTile + wave * 32 + src_lane;
-        const int64_t trow = static_cast<int64_t>(b) * P.x_stride + static_cast<int64_t>(tok) * D;
-        uint64_t best = ~0ull;
-        for (int j0 = 0; j0 < K; j0 += kWave) {
-            const int j = j0 + lane;
-            if (j < K) {
-                const float* c = cent + static_cast<int64_t>(j) * D;
-                float dot = 0.0f;
-                for (int d = 0; d < D; d += 4) {
-                    const f32x4 cv = *reinterpret_cast<const f32x4*>(c + d);
-                    dot = fmaf(load_elem<DT>(P.x, trow + d + 0), cv[0], dot);
-                    dot = fmaf(load_elem<DT>(P.x, trow + d + 1), cv[1], dot);
-                    dot = fmaf(load_elem<DT>(P.x, trow + d + 2), cv[2], dot);
-                    dot = fmaf(load_elem<DT>(P.x, trow + d + 3), cv[3], dot);
-                }
-                const float dist = fmaf(-2.0f, dot, norms[j]);
-                const uint64_t key = (static_cast<uint64_t>(orderable(dist)) << 32) | static_cast<uint32_t>(j);
-                best = key < best ? key : best;
-            }
-        }
 #pragma unroll
-        for (int m = 1; m < kWave; m <<= 1) {
-            const uint64_t o = __shfl_xor(best, m, kWave);
-            best = o < best ? o : best;
+    for (int c = 0; c < 2; ++c) {
+        // Merge the two lane halves that hold the same token.
+        const float pm1 = __shfl_xor(m1[c], 32, kWave);
+        const float pm2 = __shfl_xor(m2[c], 32, kWave);
+        const int pid = __shfl_xor(id1[c], 32, kWave);
+        const float nm2 = fminf(fminf(m2[c], pm2), fmaxf(m1[c], pm1));
+        float best = m1[c];
+        int label = id1[c];
+        if (pm1 < best || (pm1 == best && pid < label)) {
+            best = pm1;
+            label = pid;
         }
-        if ((lane % 32) == src_lane) label = static_cast<int>(best & 0xffffffffu);
-    }
-    if (valid && h == 0) {
-        P.labels[row] = label;
-        atomicAdd(P.tile_hist + (static_cast<int64_t>(b) * P.sort_tiles + t / kSortTile) * K + label, 1);
+        // Certified decision: gap > 2E proves `label` is the canonical argmin.
+        const float xnorm = sqrtf(sq[c]) * 1.001f;
+        const float thr = 1.05f * (2.0f * a.kappa * xnorm * cmax) +
+                          4.0f * 5.9604645e-8f * (fabsf(best) + fabsf(nm2)) + 1e-30f;
+        const bool flagged = valid[c] && !((nm2 - best) > thr);
+        // Canonical re-evaluation of flagged tokens, one token at a time per wave.
+        uint64_t pending = __ballot(flagged && h == 0);
+        while (pending) {
+            const int src_lane = __builtin_ctzll(pending);
+            pending &= pending - 1;
+            const int t = tile * kAssignTile + wave * 64 + 32 * c + src_lane;
+            const int64_t trow = static_cast<int64_t>(b) * P.x_stride + static_cast<int64_t>(t) * D;
+            uint64_t bestkey = ~0ull;
+            for (int j0 = 0; j0 < K; j0 += kWave) {
+                const int j = j0 + lane;
+                if (j < K) {
+                    const float* cr = cent + static_cast<int64_t>(j) * D;
+                    float dot = 0.0f;
+                    for (int d = 0; d < D; d += 4) {
+                        const f32x4 cv = *reinterpret_cast<const f32x4*>(cr + d);
+                        dot = fmaf(load_elem<DT>(P.x, trow + d + 0), cv[0], dot);
+                        dot = fmaf(load_elem<DT>(P.x, trow + d + 1), cv[1], dot);
+                        dot = fmaf(load_elem<DT>(P.x, trow + d + 2), cv[2], dot);
+                        dot = fmaf(load_elem<DT>(P.x, trow + d + 3), cv[3], dot);
+                    }
+                    const float dist = fmaf(-2.0f, dot, norms[j]);
+                    const uint64_t key = (static_cast<uint64_t>(orderable(dist)) << 32) | static_cast<uint32_t>(j);
+                    bestkey = key < bestkey ? key : bestkey;
+                }
+            }
+#pragma unroll
+            for (int m = 1; m < kWave; m <<= 1) {
+                const uint64_t o = __shfl_xor(bestkey, m, kWave);
+                bestkey = o < bestkey ? o : bestkey;
+            }
+            if ((lane % 32) == src_lane) label = static_cast<int>(bestkey & 0xffffffffu);
+        }
+        if (valid[c] && h == 0) {
+            P.labels[static_cast<int64_t>(b) * P.tokens + tok[c]] = label;
+            atomicAdd(P.tile_hist + (static_cast<int64_t>(b) * P.sort_tiles + tok[c] / kSortTile) * K + label, 1);
+        }
     }
 }
 
@@ -314,24 +384,32 @@ __global__ __launch_bounds__(64) void km_update_kernel(KmArgs a, KmIter it) {
     float s[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) s[i] = 0.0f;
-    int m = begin;
-    for (; m + 4 <= end; m += 4) {
-        float v[4][PER];
+    // Member indices arrive 64 at a time (one per lane) and are broadcast with readlane;
+    // 16 row loads are in flight before their adds, which stay in member (= token) order.
+    for (int m0 = begin; m0 < end; m0 += kWave) {
+        const int cnt = min(kWave, end - m0);
+        const int mine = lane < cnt ? idx[m0 + lane] : 0;
+        int j = 0;
+        for (; j + 16 <= cnt; j += 16) {
+            float v[16][PER];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int64_t e = xbase + static_cast<int64_t>(idx[m + u]) * D;
+            for (int u = 0; u < 16; ++u) {
+                const int t = __builtin_amdgcn_readlane(mine, j + u);
+                const int64_t e = xbase + static_cast<int64_t>(t) * D;
 #pragma unroll
-            for (int i = 0; i < PER; ++i) v[u][i] = load_elem<DT>(P.x, e + i);
+                for (int i = 0; i < PER; ++i) v[u][i] = load_elem<DT>(P.x, e + i);
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u)
+#pragma unroll
+                for (int i = 0; i < PER; ++i) s[i] = s[i] + v[u][i];
         }
+        for (; j < cnt; ++j) {
+            const int t = __builtin_amdgcn_readlane(mine, j);
+            const int64_t e = xbase + static_cast<int64_t>(t) * D;
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-            for (int i = 0; i < PER; ++i) s[i] = s[i] + v[u][i];
-    }
-    for (; m < end; ++m) {
-        const int64_t e = xbase + static_cast<int64_t>(idx[m]) * D;
-#pragma unroll
-        for (int i = 0; i < PER; ++i) s[i] = s[i] + load_elem<DT>(P.x, e + i);
+            for (int i = 0; i < PER; ++i) s[i] = s[i] + load_elem<DT>(P.x, e + i);
+        }
     }
     const int count = end - begin;
     const int64_t cbase = static_cast<int64_t>(local) * D + lane * PER;

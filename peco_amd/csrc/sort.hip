@@ -141,9 +141,18 @@ __global__ __launch_bounds__(64) void sort_place_kernel(SortArgs args) {
     const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
     const int begin = tile * kSortTile;
     const int end = min(P.tokens, begin + kSortTile);
-    for (int step = begin; step < end; step += kWave) {
-        const int t = step + lane;
-        const int raw = t < end ? lab[t] : 0;
+    // All labels of the tile are loaded before ranking starts (16 independent loads per lane).
+    constexpr int kSteps = kSortTile / kWave;
+    int labs[kSteps];
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st) {
+        const int t = begin + st * kWave + lane;
+        labs[st] = t < end ? lab[t] : -1;
+    }
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st) {
+        const int t = begin + st * kWave + lane;
+        const int raw = labs[st];
         const bool active = t < end && static_cast<unsigned>(raw) < static_cast<unsigned>(K);
         const int L = active ? raw : 0;
         uint64_t eq = __ballot(active);
