@@ -22,7 +22,7 @@ from pathlib import Path
 PACKAGE = Path(__file__).resolve().parent
 CSRC = PACKAGE / "csrc"
 LIB_DIR = PACKAGE / "_lib"
-LIB_PATH = LIB_DIR / "libpeco_hip.so"
+LIB_PATH = Path(os.environ.get("PECO_HIP_LIBRARY", LIB_DIR / "libpeco_hip.so"))
 ARCH = os.environ.get("PECO_OFFLOAD_ARCH", "gfx950")
 
 HIP_FLAGS = [

@@ -26,6 +26,7 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace peco {
 namespace {
@@ -215,6 +216,12 @@ template <> struct Mfma<kBF16> {
         typedef float f2 __attribute__((ext_vector_type(2)));
         return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, b2));
     }
+    // acc + lo(p) + hi(p) of a packed pair (v_dot2_f32_bf16 against (1, 1)).
+    static __device__ __forceinline__ float sum2(uint32_t p, float acc) {
+        typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, p), __builtin_bit_cast(b2, 0x3f803f80u), acc,
+                                               false);
+    }
 };
 template <> struct Mfma<kF16> {
     static __device__ __forceinline__ f32x16 run(u16x8 a, u16x8 b, f32x16 c) {
@@ -225,6 +232,10 @@ template <> struct Mfma<kF16> {
         typedef _Float16 h2 __attribute__((ext_vector_type(2)));
         typedef float f2 __attribute__((ext_vector_type(2)));
         return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, h2));
+    }
+    static __device__ __forceinline__ float sum2(uint32_t p, float acc) {
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, p), __builtin_bit_cast(h2, 0x3c003c00u), acc, false);
     }
 };
 
@@ -362,8 +373,8 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     if (ntiles > 0) load_tile_lds<D>(ks[0], vs[0], kh, vh, prow[0], wave, lane);
     __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0): this wave's tile-0 loads have landed
     __syncthreads();
-    for (int tile = 0; tile < ntiles; ++tile) {
-        const int buf = tile & 1;
+    auto step = [&](auto bufc, int tile) {
+        constexpr int buf = decltype(bufc)::value;
         const bool more = tile + 1 < ntiles;
         if (more) load_tile_lds<D>(ks[buf ^ 1], vs[buf ^ 1], kh, vh, prow[buf ^ 1], wave, lane);
         if (wave_active) {
@@ -371,26 +382,30 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
             const bool partial = base + kKTile > L;
             const uint16_t* kt = ks[buf];
             const uint16_t* vt = vs[buf];
+            // S^T for both 32-key halves first, so the softmax of one half overlaps MFMAs.
+            f32x16 sacc[2] = {f32x16{}, f32x16{}};
 #pragma unroll
             for (int cb = 0; cb < 2; ++cb) {
-                f32x16 sacc = {};
                 const int krow = 32 * cb + arow;
 #pragma unroll
                 for (int s = 0; s < S; ++s) {
                     const int pc = (2 * s + h) ^ T::swz_k(krow);
                     const u16x8 kf = *reinterpret_cast<const u16x8*>(kt + krow * D + pc * 8);
-                    sacc = Mfma<DT>::run(kf, qf[s], sacc);
+                    sacc[cb] = Mfma<DT>::run(kf, qf[s], sacc[cb]);
                 }
+            }
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
                 if (partial) {
 #pragma unroll
                     for (int i = 0; i < 16; ++i) {
                         const int key = base + 32 * cb + 8 * (i / 4) + 4 * h + (i % 4);
-                        if (key >= L) sacc[i] = -INFINITY;
+                        if (key >= L) sacc[cb][i] = -INFINITY;
                     }
                 }
-                float tmax = sacc[0];
+                float tmax = sacc[cb][0];
 #pragma unroll
-                for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, sacc[i]);
+                for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, sacc[cb][i]);
                 tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
                 if (__any(tmax > m_run + lazy)) {
                     const float m_new = fmaxf(m_run, tmax);
@@ -403,17 +418,14 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
 #pragma unroll
                         for (int i = 0; i < 16; ++i) oacc[nb][i] *= alpha;
                 }
-                float psum = 0.0f;
                 uint32_t pp[8];
 #pragma unroll
                 for (int i = 0; i < 16; i += 2) {
-                    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[i], scale_log2, neg_m));
-                    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[i + 1], scale_log2, neg_m));
-                    psum += p0;
-                    psum += p1;
+                    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[cb][i], scale_log2, neg_m));
+                    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[cb][i + 1], scale_log2, neg_m));
                     pp[i / 2] = Mfma<DT>::pack2(p0, p1);
+                    l_run = Mfma<DT>::sum2(pp[i / 2], l_run);
                 }
-                l_run += psum;
                 // O^T += V^T P^T over the two 16-key k-steps of this 32-key half. The V^T
                 // fragment (channel 32nb + l%32, 8 keys) comes from two transpose reads: source
                 // lane r of each 16-lane group points at key 32cb+16kk+8t+4h+r/4, channels
@@ -448,6 +460,10 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
         }
         __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of the next tile have landed
         __syncthreads();
+    };
+    for (int tile = 0; tile < ntiles; tile += 2) {
+        step(std::integral_constant<int, 0>{}, tile);
+        if (tile + 1 < ntiles) step(std::integral_constant<int, 1>{}, tile + 1);
     }
     if (!qvalid) return;
     const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);

@@ -9,14 +9,17 @@
 //   sum_j = fp32 adds of member rows in original token order   (== torch scatter_add_)
 //
 // Assignment never evaluates D_tj for every pair. A bf16 MFMA screen computes
-//   S_tj = x_t . (c_hi + c_lo)*(-2)   with c_hi = bf16(c), c_lo = bf16(c - c_hi)
-// (x itself is split the same way when it is not bf16), whose error against the exact
-// dot product is bounded a priori (|c - c_hi - c_lo| <= 2^-16 |c|, products exact in fp32,
-// fp32 accumulation error <= gamma_n). With screened minimum m1 (at id1), second minimum m2
-// and the bound E on |screened - canonical| for any centre, m2 - m1 > 2E proves that id1 is
-// the canonical argmin. Tokens that fail the test are re-evaluated in-kernel with the
-// canonical fp32 formula over all centres. Labels are therefore identical to the canonical
-// fixed-order fp32 definition, not approximately equal.
+//   S_tj = |c_j|^2 + x_t . (c_hi + c_lo)*(-2)   with c_hi = bf16(c), c_lo = bf16(c - c_hi)
+// (x itself is split the same way when it is not bf16), whose error against the canonical
+// distance is bounded a priori (|c - c_hi - c_lo| <= 2^-16 |c|, products exact in fp32,
+// fp32 accumulation error <= gamma_n, canonical chain error <= gamma_D). Each token keeps
+// its four smallest screened values with the centre index packed into the low mantissa
+// bits. With best and second best b1 <= b2 and the bound E, b2 - b1 > 2E proves that the
+// centre of b1 is the canonical argmin. Otherwise every centre screening within b1 + 2E is
+// a candidate (all of them are among the kept four unless that list is saturated); the
+// candidates get the canonical fp32 distance in-kernel, lowest index on ties, and a
+// saturated list falls back to evaluating all centres. Labels are therefore identical to the
+// canonical fixed-order fp32 definition, not approximately equal.
 //
 // Per iteration: assign (+ per-tile label histogram via global atomics) -> sort scan ->
 // sort place (stable counting sort, also yields the final permutation for stage 3) ->
@@ -60,7 +63,8 @@ struct KmArgs {
     int num;
     int total_assign_blocks;
     int total_update_blocks;
-    float kappa;  // bound coefficient: |screened - canonical| <= kappa*|x||c| + rounding terms
+    float kappa;      // bound coefficient: |screened - canonical| <= kappa*|x||c| + rounding terms
+    float gamma_acc;  // gamma of the MFMA accumulation length (applied to the norm term)
 };
 
 struct KmIter {
@@ -167,6 +171,9 @@ __device__ __forceinline__ void load_x8(const void* x, int64_t e, bool valid, u1
 // 32 (split-bf16 hi/lo rows + canonical norms), double-buffered with a register prefetch.
 // MFMA 32x32x16: A = centres (32 rows x 16 channels), B = tokens (16 channels x 32 tokens);
 // lane l holds token l%32 of each column block and centres 8*(i/4)+4*(l/32)+i%4.
+// Screened distance of centres past K (finite, so index bits can be packed into it).
+constexpr float kFarAway = 1.0e37f;
+
 template <int D> struct AssignTiles {
     static constexpr int kRow = D + 8;                 // padded LDS row (16-bit elements)
     static constexpr int kElems = 32 * kRow;
@@ -191,7 +198,7 @@ __device__ __forceinline__ void load_centres(CentreRegs<D>& R, const uint16_t* h
         R.hi[i] = *reinterpret_cast<const u32x4*>(hi_base + e);
         R.lo[i] = *reinterpret_cast<const u32x4*>(lo_base + e);
     }
-    if (tid < 32) R.norm = cb + tid < K ? norms[cb + tid] : INFINITY;
+    if (tid < 32) R.norm = cb + tid < K ? norms[cb + tid] : kFarAway;
 }
 
 template <int D>
@@ -205,6 +212,42 @@ __device__ __forceinline__ void store_centres(const CentreRegs<D>& R, uint16_t* 
         *reinterpret_cast<u32x4*>(lo + off) = R.lo[i];
     }
     if (tid < 32) nrm[tid] = R.norm;
+}
+
+// Canonical dot x_t . c_j: fma chain over d ascending (the oracle's order). Loads go out
+// 32 channels at a time so a dot costs D/32 memory latencies, not D.
+template <int DT, int D>
+__device__ __forceinline__ float canonical_dot(const void* x, int64_t xrow, const float* c) {
+    float dot = 0.0f;
+#pragma unroll
+    for (int d0 = 0; d0 < D; d0 += 32) {
+        float xv[32], cv[32];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            float tmp[8];
+            if constexpr (DT == kF32) {
+                const f32x4 a0 = *reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + xrow + d0 + 8 * q);
+                const f32x4 a1 = *reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + xrow + d0 + 8 * q + 4);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) { tmp[e] = a0[e]; tmp[4 + e] = a1[e]; }
+            } else {
+                const u16x8 u = *reinterpret_cast<const u16x8*>(static_cast<const uint16_t*>(x) + xrow + d0 + 8 * q);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) tmp[e] = half_to_f32<DT == kBF16 ? kBF16 : kF16>(u[e]);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xv[8 * q + e] = tmp[e];
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const f32x4 cq = *reinterpret_cast<const f32x4*>(c + d0 + 4 * q);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) cv[4 * q + e] = cq[e];
+        }
+#pragma unroll
+        for (int e = 0; e < 32; ++e) dot = fmaf(xv[e], cv[e], dot);
+    }
+    return dot;
 }
 
 template <int DT, int D>
@@ -258,14 +301,31 @@ __global__ __launch_bounds__(256, 2) void km_assign_kernel(KmArgs a, KmIter it) 
     __syncthreads();
     nmax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 
-    float m1[2] = {INFINITY, INFINITY}, m2[2] = {INFINITY, INFINITY};
-    int id1[2] = {0, 0};
+    // Sorted four smallest screened values per token (t[0] <= ... <= t[3]). The centre index
+    // j is packed into the low `ibits` mantissa bits, so min/med3 track value and index
+    // together; the packing error is part of the certification bound below.
+    const int ibits = 32 - __builtin_clz(static_cast<unsigned>(max(K - 1, 1)));
+    const uint32_t imask = (1u << ibits) - 1u;
+    float t[2][4];
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) t[c][k] = kFarAway;
     const int nblocks = static_cast<int>(ceil_div(K, 32));
     for (int blk = 0; blk < nblocks; ++blk) {
         const int buf = blk & 1;
         const bool more = blk + 1 < nblocks;
         if (more) load_centres<D>(regs, hi_base, lo_base, norms, (blk + 1) * 32, K, tid);
-        f32x16 acc[2] = {f32x16{}, f32x16{}};
+        // Accumulators start at the centre norms: acc = |c|^2 - 2 x.c after the chain.
+        f32x16 acc[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 n4 = *reinterpret_cast<const f32x4*>(&cn[buf][8 * g + 4 * h]);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[c][4 * g + r] = n4[r];
+            }
         const uint16_t* hrow = chi[buf] + (lane % 32) * T::kRow + 8 * h;
         const uint16_t* lrow = clo[buf] + (lane % 32) * T::kRow + 8 * h;
 #pragma unroll
@@ -281,23 +341,16 @@ __global__ __launch_bounds__(256, 2) void km_assign_kernel(KmArgs a, KmIter it) 
             }
         }
         const int cb = blk * 32;
-        float nv[16];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const f32x4 n4 = *reinterpret_cast<const f32x4*>(&cn[buf][8 * g + 4 * h]);
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t j = static_cast<uint32_t>(cb + 8 * (i / 4) + 4 * h + (i % 4));
 #pragma unroll
-            for (int r = 0; r < 4; ++r) nv[4 * g + r] = n4[r];
-        }
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int j = cb + 8 * (i / 4) + 4 * h + (i % 4);
-                const float v = acc[c][i] + nv[i];  // +inf for centres past K
-                const float nm2 = fminf(m2[c], fmaxf(m1[c], v));
-                id1[c] = v < m1[c] ? j : id1[c];
-                m1[c] = fminf(m1[c], v);
-                m2[c] = nm2;
+            for (int c = 0; c < 2; ++c) {
+                const float v = __uint_as_float((__float_as_uint(acc[c][i]) & ~imask) | j);
+                t[c][3] = __builtin_amdgcn_fmed3f(t[c][2], v, t[c][3]);
+                t[c][2] = __builtin_amdgcn_fmed3f(t[c][1], v, t[c][2]);
+                t[c][1] = __builtin_amdgcn_fmed3f(t[c][0], v, t[c][1]);
+                t[c][0] = fminf(t[c][0], v);
             }
         }
         if (more) store_centres<D>(regs, chi[buf ^ 1], clo[buf ^ 1], cn[buf ^ 1], tid);
@@ -306,56 +359,49 @@ __global__ __launch_bounds__(256, 2) void km_assign_kernel(KmArgs a, KmIter it) 
 
     const float cmax = sqrtf(nmax) * 1.001f;
     const float* cent = it.src[p] + static_cast<int64_t>(b) * K * D;
+    // Index packing perturbs a value by < 2^ibits ulp.
+    const float pack_rel = 1.01f * __uint_as_float((127u - 23u + static_cast<uint32_t>(ibits)) << 23);
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-        // Merge the two lane halves that hold the same token.
-        const float pm1 = __shfl_xor(m1[c], 32, kWave);
-        const float pm2 = __shfl_xor(m2[c], 32, kWave);
-        const int pid = __shfl_xor(id1[c], 32, kWave);
-        const float nm2 = fminf(fminf(m2[c], pm2), fmaxf(m1[c], pm1));
-        float best = m1[c];
-        int label = id1[c];
-        if (pm1 < best || (pm1 == best && pid < label)) {
-            best = pm1;
-            label = pid;
-        }
-        // Certified decision: gap > 2E proves `label` is the canonical argmin.
+        // The two lane halves of a token hold disjoint centres; combine their lists.
+        float pt[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) pt[k] = __shfl_xor(t[c][k], 32, kWave);
+        const float best = fminf(t[c][0], pt[0]);
+        const float second = fminf(fmaxf(t[c][0], pt[0]), fminf(t[c][1], pt[1]));
+        int label = static_cast<int>(__float_as_uint(best) & imask);
+        // Certified decision: gap > thr (= 2E) proves `label` is the canonical argmin. E covers
+        // the split-bf16 screen and the canonical fma chain (kappa), the norm inside the MFMA
+        // accumulation (gamma_acc * |c|^2), fp32 rounding and the index packing.
         const float xnorm = sqrtf(sq[c]) * 1.001f;
-        const float thr = 1.05f * (2.0f * a.kappa * xnorm * cmax) +
-                          4.0f * 5.9604645e-8f * (fabsf(best) + fabsf(nm2)) + 1e-30f;
-        const bool flagged = valid[c] && !((nm2 - best) > thr);
-        // Canonical re-evaluation of flagged tokens, one token at a time per wave.
-        uint64_t pending = __ballot(flagged && h == 0);
-        while (pending) {
-            const int src_lane = __builtin_ctzll(pending);
-            pending &= pending - 1;
-            const int t = tile * kAssignTile + wave * 64 + 32 * c + src_lane;
-            const int64_t trow = static_cast<int64_t>(b) * P.x_stride + static_cast<int64_t>(t) * D;
-            uint64_t bestkey = ~0ull;
-            for (int j0 = 0; j0 < K; j0 += kWave) {
-                const int j = j0 + lane;
-                if (j < K) {
-                    const float* cr = cent + static_cast<int64_t>(j) * D;
-                    float dot = 0.0f;
-                    for (int d = 0; d < D; d += 4) {
-                        const f32x4 cv = *reinterpret_cast<const f32x4*>(cr + d);
-                        dot = fmaf(load_elem<DT>(P.x, trow + d + 0), cv[0], dot);
-                        dot = fmaf(load_elem<DT>(P.x, trow + d + 1), cv[1], dot);
-                        dot = fmaf(load_elem<DT>(P.x, trow + d + 2), cv[2], dot);
-                        dot = fmaf(load_elem<DT>(P.x, trow + d + 3), cv[3], dot);
-                    }
-                    const float dist = fmaf(-2.0f, dot, norms[j]);
-                    const uint64_t key = (static_cast<uint64_t>(orderable(dist)) << 32) | static_cast<uint32_t>(j);
-                    bestkey = key < bestkey ? key : bestkey;
+        const float thr = 1.05f * (2.0f * a.kappa * xnorm * cmax + 2.0f * a.gamma_acc * nmax) +
+                          (4.0f * 5.9604645e-8f + pack_rel) * (fabsf(best) + fabsf(second)) + 1e-30f;
+        const bool flagged = valid[c] && !((second - best) > thr);
+        // Every centre that can still be the canonical argmin screens within `bound`. If a
+        // lane's four smallest all fall inside, its list may have missed one (saturated).
+        const float bound = best + thr;
+        const bool saturated = flagged && (t[c][3] <= bound || pt[3] <= bound);
+        const int64_t trow = static_cast<int64_t>(b) * P.x_stride + static_cast<int64_t>(tok[c]) * D;
+        uint64_t key = ~0ull;
+        if (flagged && !saturated) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if (t[c][k] <= bound) {
+                    const int j = static_cast<int>(__float_as_uint(t[c][k]) & imask);
+                    const float dist = fmaf(-2.0f, canonical_dot<DT, D>(P.x, trow, cent + static_cast<int64_t>(j) * D),
+                                            norms[j]);
+                    const uint64_t kj = (static_cast<uint64_t>(orderable(dist)) << 32) | static_cast<uint32_t>(j);
+                    key = kj < key ? kj : key;
                 }
             }
-#pragma unroll
-            for (int m = 1; m < kWave; m <<= 1) {
-                const uint64_t o = __shfl_xor(bestkey, m, kWave);
-                bestkey = o < bestkey ? o : bestkey;
-            }
-            if ((lane % 32) == src_lane) label = static_cast<int>(bestkey & 0xffffffffu);
         }
+        {
+            const uint64_t other = __shfl_xor(key, 32, kWave);
+            key = other < key ? other : key;
+        }
+        if (flagged && !saturated) label = static_cast<int>(key & 0xffffffffu);
+        // Rare fallback: canonical re-evaluation of a saturated token over all centres.
+        uint64_t pending = __ballot(saturated && h == 0);
         if (valid[c] && h == 0) {
             P.labels[static_cast<int64_t>(b) * P.tokens + tok[c]] = label;
             atomicAdd(P.tile_hist + (static_cast<int64_t>(b) * P.sort_tiles + tok[c] / kSortTile) * K + label, 1);
@@ -537,6 +583,7 @@ hipError_t km_fit(const KmFitDesc* descs, int num, int dims, int dtype, int iter
     a.total_assign_blocks = ab;
     a.total_update_blocks = ub;
     a.kappa = km_kappa(dtype, dims);
+    a.gamma_acc = static_cast<float>(gamma_n(3.0 * dims + 2));
     sort_args_finalize(sa);
     std::vector<KmIter> iters(std::max(iterations, 1));
     for (int i = 0; i < iterations; ++i) {
@@ -637,6 +684,7 @@ PECO_API int peco_assign_tokens_to_centers(const float* x, const float* centers,
     a.total_assign_blocks = batch * static_cast<int>(ceil_div(tokens, kAssignTile));
     a.total_update_blocks = batch * clusters;
     a.kappa = km_kappa(kF32, dims);
+    a.gamma_acc = static_cast<float>(gamma_n(3.0 * dims + 2));
     KmIter it{};
     it.src[0] = centers;
     if (dims == 128) {
