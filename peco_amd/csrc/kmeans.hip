@@ -409,6 +409,19 @@ __global__ __launch_bounds__(256, 2) void km_assign_kernel(KmArgs a, KmIter it) 
     }
 }
 
+// PER consecutive channels of one row as fp32 (one 32-bit load for two 16-bit channels).
+template <int DT, int PER>
+__device__ __forceinline__ void load_pair(const void* x, int64_t e, float (&v)[PER]) {
+    if constexpr (PER == 2 && DT != kF32) {
+        const uint32_t w = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(x) + e);
+        v[0] = half_to_f32<DT == kBF16 ? kBF16 : kF16>(static_cast<uint16_t>(w & 0xffffu));
+        v[1] = half_to_f32<DT == kBF16 ? kBF16 : kF16>(static_cast<uint16_t>(w >> 16));
+    } else {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) v[i] = load_elem<DT>(x, e + i);
+    }
+}
+
 // Update: one wavefront per (problem, batch, cluster). Sums member rows in original token
 // order (the sorted member list is stable), divides by the count, and prepares the next
 // iteration's split centres and canonical norm.
@@ -430,31 +443,44 @@ __global__ __launch_bounds__(64) void km_update_kernel(KmArgs a, KmIter it) {
     float s[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) s[i] = 0.0f;
-    // Member indices arrive 64 at a time (one per lane) and are broadcast with readlane;
-    // 16 row loads are in flight before their adds, which stay in member (= token) order.
+    // Member indices arrive 64 at a time (one per lane) and are broadcast with readlane; all
+    // of a chunk's row loads (32 bits per lane) are in flight before the adds, which stay in
+    // member (= token) order.
     for (int m0 = begin; m0 < end; m0 += kWave) {
         const int cnt = min(kWave, end - m0);
-        const int mine = lane < cnt ? idx[m0 + lane] : 0;
-        int j = 0;
-        for (; j + 16 <= cnt; j += 16) {
-            float v[16][PER];
+        const int mine = lane < cnt ? idx[m0 + lane] : idx[m0];
+        if (cnt == kWave) {
+            float v[kWave][PER];
 #pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                const int t = __builtin_amdgcn_readlane(mine, j + u);
-                const int64_t e = xbase + static_cast<int64_t>(t) * D;
-#pragma unroll
-                for (int i = 0; i < PER; ++i) v[u][i] = load_elem<DT>(P.x, e + i);
+            for (int u = 0; u < kWave; ++u) {
+                const int t = __builtin_amdgcn_readlane(mine, u);
+                load_pair<DT, PER>(P.x, xbase + static_cast<int64_t>(t) * D, v[u]);
             }
 #pragma unroll
-            for (int u = 0; u < 16; ++u)
+            for (int u = 0; u < kWave; ++u)
 #pragma unroll
                 for (int i = 0; i < PER; ++i) s[i] = s[i] + v[u][i];
-        }
-        for (; j < cnt; ++j) {
-            const int t = __builtin_amdgcn_readlane(mine, j);
-            const int64_t e = xbase + static_cast<int64_t>(t) * D;
+        } else {
+            int j = 0;
+            for (; j + 16 <= cnt; j += 16) {
+                float v[16][PER];
 #pragma unroll
-            for (int i = 0; i < PER; ++i) s[i] = s[i] + load_elem<DT>(P.x, e + i);
+                for (int u = 0; u < 16; ++u) {
+                    const int t = __builtin_amdgcn_readlane(mine, j + u);
+                    load_pair<DT, PER>(P.x, xbase + static_cast<int64_t>(t) * D, v[u]);
+                }
+#pragma unroll
+                for (int u = 0; u < 16; ++u)
+#pragma unroll
+                    for (int i = 0; i < PER; ++i) s[i] = s[i] + v[u][i];
+            }
+            for (; j < cnt; ++j) {
+                const int t = __builtin_amdgcn_readlane(mine, j);
+                float v[PER];
+                load_pair<DT, PER>(P.x, xbase + static_cast<int64_t>(t) * D, v);
+#pragma unroll
+                for (int i = 0; i < PER; ++i) s[i] = s[i] + v[i];
+            }
         }
     }
     const int count = end - begin;

@@ -164,14 +164,18 @@ __global__ __launch_bounds__(64) void sort_place_kernel(SortArgs args) {
         const int rank = __popcll(eq & below);
         const int total = __popcll(eq);
         const bool last = active && ((eq >> lane) == 1ull);
+        // One wavefront: its LDS reads and writes execute in program order, so the read of
+        // base[L] above precedes the update below without a workgroup barrier (whose memory
+        // fence would also wait for the scattered global stores every step).
+        int pos = 0;
+        if (active) pos = base[L] + rank;
+        __builtin_amdgcn_wave_barrier();
+        if (last) base[L] += total;
+        __builtin_amdgcn_wave_barrier();
         if (active) {
-            const int pos = base[L] + rank;
             idx[pos] = t;
             if (ranks) ranks[t] = pos;
         }
-        __syncthreads();
-        if (last) base[L] += total;
-        __syncthreads();
     }
 }
 
