@@ -40,6 +40,13 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--stage-reps", type=int, default=10)
+    ap.add_argument("--profile-target", choices=("attention", "copy"), default=None,
+                    help="replay only the attention launch, or a plain device copy of --copy-mib MiB, --reps times "
+                         "(for rocprofv3 counter runs)")
+    ap.add_argument("--reps", type=int, default=10)
+    ap.add_argument("--copy-mib", type=int, default=1024)
+    ap.add_argument("--summarize", metavar="CSV", default=None,
+                    help="print per-kernel averages of a rocprofv3 counter_collection.csv or kernel_stats.csv")
     return ap.parse_args()
 
 
@@ -116,6 +123,17 @@ def attention_kernel_time(args_, reps=20):
     return start.elapsed_time(end) / reps
 
 
+def measured_traffic(workload):
+    """HBM bytes per attention launch from the committed rocprofv3 counter summary, if any."""
+    import re
+
+    path = ROOT / "profiles" / f"sparse_attention_{workload}_traffic.txt"
+    if not path.exists():
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", path.read_text(), re.M)
+    return float(m.group(1)) if m else None
+
+
 def cpu_baseline(wl, budget_s):
     """Oracle (reference CPU torch path) on whole heads of the workload until the budget is spent."""
     from oracle import reference_path
@@ -144,8 +162,59 @@ def cpu_baseline(wl, budget_s):
                       f"layer {1e3 * elapsed / done * s.heads:.1f} ms extrapolated to {s.heads} heads"}
 
 
+def summarize(path):
+    """Per-kernel averages from a rocprofv3 CSV (counter collection or kernel stats)."""
+    import csv
+    from collections import defaultdict
+
+    rows = list(csv.DictReader(open(path)))
+    if rows and "Counter_Name" in rows[0]:
+        acc = defaultdict(lambda: defaultdict(float))
+        disp = defaultdict(set)
+        for r in rows:
+            name = r["Kernel_Name"].replace("(anonymous namespace)::", "").split("(")[0]
+            acc[name][r["Counter_Name"]] += float(r["Counter_Value"])
+            disp[name].add(r["Dispatch_Id"])
+        for name, counters in acc.items():
+            n = len(disp[name])
+            vals = ", ".join(f"{k}={v / n:.6g}" for k, v in sorted(counters.items()))
+            print(f"{name}: dispatches={n} per-dispatch {vals}")
+    else:
+        for r in rows[:20]:
+            print(",".join(r.values()))
+
+
+def profile_target(args):
+    dev = torch.device("cuda:0")
+    if args.profile_target == "copy":
+        n = args.copy_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(args.reps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"copy {args.copy_mib} MiB x {args.reps}: reads {args.copy_mib * 1024} KiB and writes "
+              f"{args.copy_mib * 1024} KiB per dispatch", flush=True)
+        return
+    from peco_amd import workloads
+
+    wl = workloads.make_workload(args.workload, device=dev)
+    layer = make_layer(wl)
+    with torch.no_grad():
+        _, flops, attn_args = stage_breakdown(layer, wl, wl.query, wl.key, wl.value, wl.q_init, wl.k_init, 1)
+        t = attention_kernel_time(attn_args, args.reps)
+    print(f"attention launch {t * 1e3:.1f} us, {flops / (t * 1e-3) / 1e12:.1f} TFLOP/s, flops {flops:.6g}",
+          flush=True)
+
+
 def main():
     args = parse()
+    if args.summarize:
+        summarize(args.summarize)
+        return
+    if args.profile_target:
+        profile_target(args)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are not part of it",
                           "n_gpus": args.gpus}))
@@ -179,7 +248,7 @@ def main():
                    "head_dim": s.dims, "q_clusters": s.num_q_centroids, "k_clusters": s.num_k_centroids,
                    "kmeans_iterations": s.iterations, "keep_ratio": s.keep_ratio, "base_offset_bits": s.bits},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic(s.name),
                      "kernel": "sparse_attention (work list + MFMA kernel)", "kernel_ms": round(t_attn, 4),
                      "flops": flops},
         "stages_ms": {k_: round(v_, 4) for k_, v_ in stages.items()},
