@@ -16,6 +16,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -69,14 +70,14 @@ def run_step(layer, wl, q, k, v, q_init, k_init):
 
 def stage_breakdown(layer, wl, q, k, v, q_init, k_init, reps):
     """Per-stage device time (ms) with events on the current stream, and the realised FLOPs."""
-    from peco_amd import attention_cuda, clustering_cuda, processor, workloads
-    from peco_amd.clustering import select_cluster_connections
+    from peco_amd import attention_cuda, clustering_cuda, workloads
 
     s = wl.shape
-    n, length, dim, heads = s.video, s.length, s.dims, s.heads
-    names = ("kmeans", "select", "pack", "partition", "attention")
+    n, dim, heads = s.video, s.dims, s.heads
+    names = ("kmeans", "select", "pack", "attention")
     acc = {k_: 0.0 for k_ in names}
     flops = 0.0
+    minimum = math.ceil(wl.min_kc_ratio * s.num_k_centroids)
     for _ in range(reps):
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
         ev[0].record()
@@ -84,40 +85,38 @@ def stage_breakdown(layer, wl, q, k, v, q_init, k_init, reps):
         ql, kl, qs, ks = layer._update_cluster_state(q[:, :, :n], k[:, :, :n])
         q_idx, k_idx = layer._last_fit
         ev[1].record()
-        dmap = select_cluster_connections(layer.q_centroids.reshape(1, heads, -1, dim),
-                                          layer.k_centroids.reshape(1, heads, -1, dim), qs, ks, wl.top_p,
-                                          wl.min_kc_ratio)
+        emap, eqs, eks = clustering_cuda.select_connections(
+            layer.q_centroids.reshape(1, heads, -1, dim), layer.k_centroids.reshape(1, heads, -1, dim), qs, ks,
+            wl.top_p, minimum, text=(s.text, s.text))
         ev[2].record()
         qp, kp, vp = clustering_cuda.pack_clustered([q, k, v], [q_idx, k_idx, k_idx], [ql, kl, None],
                                                     [layer.q_centroids, layer.k_centroids, None], [s.bits, s.bits, 0],
                                                     n)
         ev[3].record()
-        emap, eqs, eks = processor._extend_partition_on_device(dmap, qs, ks, s.text, s.text)
-        idx = torch.empty((heads, length), dtype=torch.int32, device=q.device)
-        idx[:, :n] = q_idx
-        idx[:, n:] = torch.arange(n, length, device=q.device, dtype=torch.int32)
+        attention_cuda.sparse_attention(qp, kp, vp, emap, eqs, eks, validate_sizes=False, out_index=q_idx,
+                                        out_index_rows=n)
         ev[4].record()
-        attention_cuda.sparse_attention(qp, kp, vp, emap, eqs, eks, validate_sizes=False, out_index=idx)
-        ev[5].record()
         torch.cuda.synchronize()
         for i, nm in enumerate(names):
             acc[nm] += ev[i].elapsed_time(ev[i + 1])
         flops = workloads.attention_flops(emap, eqs, eks, dim)
-    return {k_: v_ / reps for k_, v_ in acc.items()}, flops, (qp, kp, vp, emap, eqs, eks, idx)
+    return {k_: v_ / reps for k_, v_ in acc.items()}, flops, (qp, kp, vp, emap, eqs, eks, q_idx, n)
 
 
 def attention_kernel_time(args_, reps=20):
     """Average duration of the sparse-attention launch (builder + kernel) on its stream."""
     from peco_amd import attention_cuda
 
-    qp, kp, vp, emap, eqs, eks, idx = args_
+    qp, kp, vp, emap, eqs, eks, idx, rows = args_
     for _ in range(3):
-        attention_cuda.sparse_attention(qp, kp, vp, emap, eqs, eks, validate_sizes=False, out_index=idx)
+        attention_cuda.sparse_attention(qp, kp, vp, emap, eqs, eks, validate_sizes=False, out_index=idx,
+                                        out_index_rows=rows)
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(reps):
-        attention_cuda.sparse_attention(qp, kp, vp, emap, eqs, eks, validate_sizes=False, out_index=idx)
+        attention_cuda.sparse_attention(qp, kp, vp, emap, eqs, eks, validate_sizes=False, out_index=idx,
+                                        out_index_rows=rows)
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / reps

@@ -103,13 +103,25 @@ int peco_pack_clustered(const void* const* inputs, void* const* outputs, const i
                         void* stream);
 
 /* peco_sparse_attention with an explicit workspace size (int32 elements, at least
- * peco_sparse_attention_workspace_size) and an optional out_index [bh, sq]: output row j
- * of head b is written to row out_index[b,j] (fuses peco/clustering.py:128-136). */
+ * peco_sparse_attention_workspace_size) and an optional out_index [bh, out_index_rows]:
+ * output row j < out_index_rows of head b is written to row out_index[b,j]; later rows keep
+ * their position (fuses peco/clustering.py:128-136 and the text rows of processor.py:153-156). */
 size_t peco_sparse_attention_workspace_size(int bh, int sq, int sk, int cq, int ck);
 int peco_sparse_attention_ex(const void* q, const void* k, const void* v, const uint8_t* selected,
                              const int* q_sizes, const int* k_sizes, void* output, const int32_t* out_index,
-                             int* workspace, size_t workspace_ints, int bh, int sq, int sk, int d, int cq, int ck,
-                             int dtype, void* stream);
+                             int out_index_rows, int* workspace, size_t workspace_ints, int bh, int sq, int sk, int d,
+                             int cq, int ck, int dtype, void* stream);
+
+/* Cluster-pair selection (replaces the torch ops of peco/clustering.py:140-186), one
+ * wavefront per query-cluster row: count-weighted softmax of centroid scores, stable
+ * descending order, keep while the preceding mass is < p (all when p == 1), at least
+ * max(1, minimum) pairs, empty clusters never pair. qc [bh,cq,dims], kc [bh,ck,dims] fp32,
+ * counts int32. With extend != 0 the map is [bh,cq+2,ck+2] with the valid-text/padding
+ * groups of peco/processor.py:68-84 and ext_q/ext_k receive the extended sizes. */
+int peco_select_cluster_connections(const float* qc, const float* kc, const int32_t* q_counts,
+                                    const int32_t* k_counts, int bh, int cq, int ck, int dims, float p, int minimum,
+                                    int extend, int valid_text, int text, uint8_t* map, int32_t* ext_q,
+                                    int32_t* ext_k, void* stream);
 
 #ifdef __cplusplus
 }

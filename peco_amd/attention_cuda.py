@@ -65,6 +65,7 @@ def sparse_attention(
     *,
     validate_sizes: bool = True,
     out_index: torch.Tensor | None = None,
+    out_index_rows: int | None = None,
 ) -> torch.Tensor:
     """Return cluster-masked softmax(QK^T/sqrt(D))V.
 
@@ -72,8 +73,9 @@ def sparse_attention(
     [B,H,CQ,CK] and int32 sizes [B,H,CQ/CK]. Tokens must already be grouped in cluster
     order. Empty clusters and completely masked rows are supported; a completely masked
     row returns zero. Sizes are checked on the stream without copying them to the host.
-    ``out_index`` (int32 [B*H, SQ], optional) writes output row j of head b to row
-    out_index[b, j] instead, fusing the inverse token permutation into the epilogue.
+    ``out_index`` (int32 [B*H, R], optional) writes output row j < R of head b to row
+    out_index[b, j] instead (rows j >= R keep their position), fusing the inverse token
+    permutation into the epilogue. R is ``out_index_rows`` (default SQ).
     """
     batch, heads, sq, dim, sk, cq, ck, stride = _validate(q, k, v, dynamic_map, q_sizes, k_sizes)
     with torch.cuda.device(q.device):
@@ -87,16 +89,19 @@ def sparse_attention(
         output = torch.empty_like(q)
         if sq == 0:
             return output
+        rows = sq if out_index_rows is None else int(out_index_rows)
         if out_index is not None:
-            if out_index.dtype != torch.int32 or out_index.numel() != batch * heads * sq or not out_index.is_contiguous():
-                raise ValueError("out_index must be a contiguous int32 tensor with B*H*SQ elements")
+            if not 0 <= rows <= sq:
+                raise ValueError("out_index_rows must be in [0, SQ]")
+            if out_index.dtype != torch.int32 or out_index.numel() != batch * heads * rows or not out_index.is_contiguous():
+                raise ValueError("out_index must be a contiguous int32 tensor with B*H*out_index_rows elements")
         # Same footprint as the reference's workspace (peco/attention_cuda.py:112-113,128).
         workspace = torch.empty(batch * heads * stride, dtype=torch.int32, device=q.device)
         library = _native.library()
         stream = _native.current_stream(q.device, q, k, v, dynamic_map, q_sizes, k_sizes, workspace, output, out_index)
         error = library.peco_sparse_attention_ex(
             _native.ptr(q), _native.ptr(k), _native.ptr(v), _native.ptr(dynamic_map), _native.ptr(q_sizes),
-            _native.ptr(k_sizes), _native.ptr(output), _native.ptr(out_index), _native.ptr(workspace),
+            _native.ptr(k_sizes), _native.ptr(output), _native.ptr(out_index), rows, _native.ptr(workspace),
             workspace.numel(), batch * heads, sq, sk, dim, cq, ck, 0 if q.dtype == torch.float16 else 1, stream,
         )
         if error:

@@ -129,25 +129,12 @@ def select_cluster_connections(query_centroids, key_centroids, q_cluster_sizes, 
     Centroids are [B,H,C,D], sizes [B,H,C]. For each query cluster keep the smallest
     descending-probability prefix reaching ``p``, and at least ceil(min_kc_ratio*CK) key
     clusters. Returns a bool [B,H,CQ,CK] map; empty clusters never pair
-    (peco/clustering.py:155-186).
+    (peco/clustering.py:155-186). Runs as one HIP launch (peco_select_cluster_connections).
     """
     if not 0 <= p <= 1 or not 0 <= min_kc_ratio <= 1:
         raise ValueError("p and min_kc_ratio must be in [0, 1]")
-    scores = torch.matmul(query_centroids.float(), key_centroids.float().transpose(-1, -2))
-    scores *= query_centroids.shape[-1] ** -0.5
-    probabilities = compute_cluster_weights(scores, k_cluster_sizes.unsqueeze(-2))
-    sorted_probs, sorted_indices = probabilities.sort(dim=-1, descending=True, stable=True)
-    cumulative_before = sorted_probs.cumsum(-1) - sorted_probs
-    # The mass before each candidate decides, so the crossing cluster is kept.
-    keep = cumulative_before < p
-    if p == 1:
-        keep.fill_(True)
-    keep[..., 0] = True
+    _require_gpu(query_centroids, key_centroids, q_cluster_sizes, k_cluster_sizes)
     minimum = math.ceil(min_kc_ratio * key_centroids.shape[-2])
-    if minimum:
-        keep[..., :minimum] = True
-    dynamic_map = torch.zeros_like(probabilities, dtype=torch.bool)
-    dynamic_map.scatter_(-1, sorted_indices, keep)
-    dynamic_map &= k_cluster_sizes.unsqueeze(-2) > 0
-    dynamic_map &= q_cluster_sizes.unsqueeze(-1) > 0
+    dynamic_map, _, _ = clustering_cuda.select_connections(query_centroids, key_centroids, q_cluster_sizes,
+                                                           k_cluster_sizes, p, minimum)
     return dynamic_map

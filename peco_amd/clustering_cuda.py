@@ -170,6 +170,41 @@ def kmeans_fit(problems, iterations):
     return outs
 
 
+def select_connections(query_centroids, key_centroids, q_counts, k_counts, p, minimum, text=None):
+    """Cluster-pair map of select_cluster_connections in one launch.
+
+    Centroids [..., C, D], counts [..., C]. With ``text=(valid_text, text_length)`` the map
+    is extended with the text partition and the extended size vectors are returned too.
+    Returns (map bool [..., CQ(+2), CK(+2)], ext_q_sizes or None, ext_k_sizes or None).
+    """
+    library = _library()
+    lead = query_centroids.shape[:-2]
+    cq, dims = query_centroids.shape[-2:]
+    ck = key_centroids.shape[-2]
+    bh = 1
+    for n in lead:
+        bh *= n
+    dev = query_centroids.device
+    qc = query_centroids.float().reshape(bh, cq, dims).contiguous()
+    kc = key_centroids.float().reshape(bh, ck, dims).contiguous()
+    qn = q_counts.to(torch.int32).reshape(bh, cq).contiguous()
+    kn = k_counts.to(torch.int32).reshape(bh, ck).contiguous()
+    extend = text is not None
+    re, ce = (cq + 2, ck + 2) if extend else (cq, ck)
+    dmap = torch.empty((*lead, re, ce), dtype=torch.bool, device=dev)
+    ext_q = torch.empty((*lead, re), dtype=torch.int32, device=dev) if extend else None
+    ext_k = torch.empty((*lead, ce), dtype=torch.int32, device=dev) if extend else None
+    valid_text, text_length = text if extend else (0, 0)
+    with torch.cuda.device(dev):
+        status = library.peco_select_cluster_connections(
+            _native.ptr(qc), _native.ptr(kc), _native.ptr(qn), _native.ptr(kn), bh, cq, ck, dims, float(p),
+            int(minimum), int(extend), int(valid_text), int(text_length), _native.ptr(dmap), _native.ptr(ext_q),
+            _native.ptr(ext_k), _retain_on_current_stream(dev, qc, kc, qn, kn, dmap, ext_q, ext_k),
+        )
+    _raise_cluster_error(status)
+    return dmap, ext_q, ext_k
+
+
 def pack_clustered(tensors, indices, labels, centroids, bits, video):
     """Gather up to three [B,H,S,D] tensors into cluster order in one launch.
 

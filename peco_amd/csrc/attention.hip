@@ -296,7 +296,7 @@ template <int DT, int D>
 __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint8_t* __restrict__ selected, const int32_t* __restrict__ ws, uint16_t* __restrict__ out,
-    const int32_t* __restrict__ out_index, int bhn, int sq, int sk, int cq, int ck, float scale_log2) {
+    const int32_t* __restrict__ out_index, int oi_rows, int bhn, int sq, int sk, int cq, int ck, float scale_log2) {
     using T = Tiles<D>;
     constexpr int S = D / 16;       // k-steps of S^T over channels
     constexpr int NB = D / 32;      // 32-channel blocks of O^T
@@ -469,7 +469,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     int64_t orow = q_start + qrow;
-    if (out_index) orow = out_index[head * sq + orow];
+    if (out_index && orow < oi_rows) orow = out_index[head * oi_rows + orow];
     uint16_t* o = out + (head * sq + orow) * D;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
@@ -501,14 +501,16 @@ PECO_API size_t peco_sparse_attention_workspace_size(int bh, int sq, int sk, int
            static_cast<size_t>(bh) * item_capacity(sq, cq) * 3;
 }
 
-// Extended entry: out_index (nullable, int32 [bh, sq]) scatters output row j of head b to
-// row out_index[b, j], fusing the inverse permutation into the epilogue.
+// Extended entry: out_index (nullable, int32 [bh, out_index_rows]) scatters output row
+// j < out_index_rows of head b to row out_index[b, j] (rows past out_index_rows keep their
+// position), fusing the inverse permutation into the epilogue.
 PECO_API int peco_sparse_attention_ex(const void* q, const void* k, const void* v, const uint8_t* selected,
                                       const int* q_sizes, const int* k_sizes, void* output, const int32_t* out_index,
-                                      int* workspace, size_t workspace_ints, int bh, int sq, int sk, int d, int cq,
-                                      int ck, int dtype, void* stream) {
+                                      int out_index_rows, int* workspace, size_t workspace_ints, int bh, int sq,
+                                      int sk, int d, int cq, int ck, int dtype, void* stream) {
     if (!q || !k || !v || !selected || !q_sizes || !k_sizes || !output || !workspace || bh < 1 || bh > 65535 ||
-        sq < 0 || sk < 0 || cq < 1 || ck < 1 || (d != 64 && d != 128) || (dtype != kF16 && dtype != kBF16))
+        sq < 0 || sk < 0 || cq < 1 || ck < 1 || (d != 64 && d != 128) || (dtype != kF16 && dtype != kBF16) ||
+        (out_index && (out_index_rows < 0 || out_index_rows > sq)))
         return kInvalidValue;
     if (sq == 0) return kOk;
     if (workspace_ints < peco_sparse_attention_workspace_size(bh, sq, sk, cq, ck)) return kWorkspaceTooSmall;
@@ -527,7 +529,7 @@ PECO_API int peco_sparse_attention_ex(const void* q, const void* k, const void* 
     auto* op = static_cast<uint16_t*>(output);
 #define PECO_ATTN(DT_, D_)                                                                                        \
     hipLaunchKernelGGL((sparse_attention_kernel<DT_, D_>), grid, dim3(256), lds_attn, s, qp, kp, vp, selected,    \
-                       workspace, op, out_index, bh, sq, sk, cq, ck, scale_log2)
+                       workspace, op, out_index, out_index_rows, bh, sq, sk, cq, ck, scale_log2)
     if (dtype == kBF16) {
         if (d == 128) PECO_ATTN(kBF16, 128);
         else PECO_ATTN(kBF16, 64);
@@ -546,6 +548,6 @@ PECO_API int peco_sparse_attention(const void* q, const void* k, const void* v, 
                                    int sq, int sk, int d, int cq, int ck, int dtype, void* stream) {
     if (bh < 1 || sq < 0) return kInvalidValue;
     const size_t ref_ints = static_cast<size_t>(bh) * (ck + 2 + 3 * (ceil_div(sq, 16) + cq));
-    return peco_sparse_attention_ex(q, k, v, selected, q_sizes, k_sizes, output, nullptr, workspace, ref_ints, bh, sq,
-                                    sk, d, cq, ck, dtype, stream);
+    return peco_sparse_attention_ex(q, k, v, selected, q_sizes, k_sizes, output, nullptr, 0, workspace, ref_ints, bh,
+                                    sq, sk, d, cq, ck, dtype, stream);
 }

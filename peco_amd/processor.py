@@ -1,17 +1,18 @@
 """HunyuanVideo attention processor with PECO cluster-sparse attention (peco/processor.py interface).
 
-The sparse path of ``PecoAttention.attention`` runs as five groups of device launches:
+The sparse path of ``PecoAttention.attention`` runs as four groups of device launches:
   1. fused Q+K k-means (clustering_cuda.kmeans_fit): labels, centres, sizes and the
      stable cluster permutation of both tensors;
-  2. cluster-pair selection (select_cluster_connections);
+  2. one selection launch: cluster-pair map with the text partition appended
+     (select_cluster_connections + extend_text_partition);
   3. one pack launch that fake-quantizes Q/K (Base-Offset, when enabled), gathers Q/K/V
      into cluster order and appends the text rows (no slice copies, no concatenations);
-  4. the text partition and restore indices (small device ops, no host copies);
-  5. the HIP work-list builder and MFMA sparse attention, whose epilogue writes every
-     row straight back to its original sequence position.
+  4. the HIP work-list builder and MFMA sparse attention, whose epilogue writes every
+     video row straight back to its original sequence position.
 """
 from __future__ import annotations
 
+import math
 from dataclasses import dataclass
 
 import torch
@@ -20,7 +21,6 @@ from torch.nn.attention import SDPBackend, sdpa_kernel
 
 from . import clustering_cuda
 from .attention_cuda import sparse_attention
-from .clustering import select_cluster_connections
 from .quantization import _validate_bits
 
 
@@ -193,23 +193,19 @@ class PecoAttention:
         q_labels, k_labels, q_sizes, k_sizes = self._update_cluster_state(
             query[:, :, :video_length], key[:, :, :video_length])
         q_idx, k_idx = self._last_fit
-        # Estimate cluster connectivity from the floating-point centres.
-        dynamic_map = select_cluster_connections(
-            self.q_centroids.reshape(batch, heads, -1, dim),
-            self.k_centroids.reshape(batch, heads, -1, dim),
-            q_sizes, k_sizes, self.config.top_p, self.config.min_kc_ratio,
-        )
+        # Cluster connectivity from the floating-point centres, extended with the text
+        # partition (select_cluster_connections + extend_text_partition in one launch).
+        dynamic_map, q_sizes, k_sizes = clustering_cuda.select_connections(
+            self.q_centroids.reshape(batch, heads, -1, dim), self.k_centroids.reshape(batch, heads, -1, dim),
+            q_sizes, k_sizes, self.config.top_p,
+            math.ceil(self.config.min_kc_ratio * self.config.num_k_centroids), text=(valid_text, text_length))
         # Fake-quantize Q/K against their centroids while packing Q/K/V into cluster order.
         q_perm, k_perm, v_perm = clustering_cuda.pack_clustered(
             [query, key, value], [q_idx, k_idx, k_idx], [q_labels, k_labels, None],
             [self.q_centroids, self.k_centroids, None], [bits, bits, 0], video_length)
-        dynamic_map, q_sizes, k_sizes = _extend_partition_on_device(
-            dynamic_map, q_sizes, k_sizes, valid_text, text_length)
-        indices = torch.empty((batch * heads, length), dtype=torch.int32, device=query.device)
-        indices[:, :video_length] = q_idx
-        indices[:, video_length:] = torch.arange(video_length, length, device=query.device, dtype=torch.int32)
+        # Video rows return to their original positions; text rows keep theirs.
         return sparse_attention(q_perm, k_perm, v_perm, dynamic_map, q_sizes, k_sizes, validate_sizes=False,
-                                out_index=indices)
+                                out_index=q_idx, out_index_rows=video_length)
 
     @torch.no_grad()
     def __call__(self, attn, hidden_states, encoder_hidden_states=None, attention_mask=None, image_rotary_emb=None):

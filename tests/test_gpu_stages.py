@@ -282,3 +282,36 @@ def test_sparse_attention_out_index_scatter(announce):
     fused = attention_cuda.sparse_attention(*args, out_index=perm.to(DEV))
     restored = clustering.restore_sequence_order(plain, perm.to(DEV))
     assert torch.equal(fused.cpu().view(torch.int16), restored.cpu().view(torch.int16))
+
+
+# ---------------------------------------------------------------- selection + text partition
+
+@pytest.mark.parametrize("p,ratio", [(1e-9, 0.25), (0.5, 0.0), (0.9, 0.1), (1.0, 0.0), (0.0, 0.0)])
+@pytest.mark.parametrize("dims,ck", [(128, 70), (64, 70), (128, 256), (128, 1000), (64, 2048)])
+def test_select_connections_matches_oracle(announce, p, ratio, dims, ck):
+    g = _gen(int(p * 100) + dims + ck)
+    b, h, cq = 1, 3, 20
+    qc = torch.randn(b, h, cq, dims, generator=g) * 0.5
+    kc = torch.randn(b, h, ck, dims, generator=g) * 0.5
+    qs = torch.randint(0, 40, (b, h, cq), generator=g, dtype=torch.int32)
+    ks = torch.randint(0, 40, (b, h, ck), generator=g, dtype=torch.int32)
+    qs[0, 0, :3] = 0
+    ks[0, 1, :5] = 0
+    announce(f"p={p} ratio={ratio} D={dims} CK={ck}")
+    m = clustering.select_cluster_connections(qc.to(DEV), kc.to(DEV), qs.to(DEV), ks.to(DEV), p, ratio)
+    ref = reference_path.select_connections(qc, kc, qs, ks, p, ratio)
+    assert torch.equal(m.cpu(), ref)
+
+
+def test_select_with_text_partition_matches_oracle(announce):
+    g = _gen(31)
+    qc = torch.randn(1, 2, 16, 128, generator=g)
+    kc = torch.randn(1, 2, 40, 128, generator=g)
+    qs = torch.randint(1, 30, (1, 2, 16), generator=g, dtype=torch.int32)
+    ks = torch.randint(0, 30, (1, 2, 40), generator=g, dtype=torch.int32)
+    announce()
+    m, eq, ek = clustering_cuda.select_connections(qc.to(DEV), kc.to(DEV), qs.to(DEV), ks.to(DEV), 1e-9, 10,
+                                                   text=(7, 9))
+    rm, rq, rk = reference_path.extend_text_partition(
+        reference_path.select_connections(qc, kc, qs, ks, 1e-9, 0.25), qs, ks, 7, 9)
+    assert torch.equal(m.cpu(), rm) and torch.equal(eq.cpu(), rq) and torch.equal(ek.cpu(), rk)
