@@ -400,8 +400,28 @@ __global__ __launch_bounds__(256, 2) void km_assign_kernel(KmArgs a, KmIter it) 
             key = other < key ? other : key;
         }
         if (flagged && !saturated) label = static_cast<int>(key & 0xffffffffu);
-        // Rare fallback: canonical re-evaluation of a saturated token over all centres.
+        // Rare fallback: canonical re-evaluation of a saturated token over all centres, one
+        // token at a time with the whole wavefront (lane i takes centres i, i + 64, ...).
         uint64_t pending = __ballot(saturated && h == 0);
+        while (pending) {
+            const int src = __builtin_ctzll(pending);  // lane (h == 0) holding the token
+            pending &= pending - 1;
+            const int64_t srow = static_cast<int64_t>(b) * P.x_stride +
+                                 static_cast<int64_t>(tile * kAssignTile + wave * 64 + 32 * c + src) * D;
+            uint64_t full = ~0ull;
+            for (int j = lane; j < K; j += kWave) {
+                const float dist =
+                    fmaf(-2.0f, canonical_dot<DT, D>(P.x, srow, cent + static_cast<int64_t>(j) * D), norms[j]);
+                const uint64_t kj = (static_cast<uint64_t>(orderable(dist)) << 32) | static_cast<uint32_t>(j);
+                full = kj < full ? kj : full;
+            }
+#pragma unroll
+            for (int m = 1; m < kWave; m <<= 1) {
+                const uint64_t other = __shfl_xor(full, m, kWave);
+                full = other < full ? other : full;
+            }
+            if (lane == src) label = static_cast<int>(full & 0xffffffffu);
+        }
         if (valid[c] && h == 0) {
             P.labels[static_cast<int64_t>(b) * P.tokens + tok[c]] = label;
             atomicAdd(P.tile_hist + (static_cast<int64_t>(b) * P.sort_tiles + tok[c] / kSortTile) * K + label, 1);

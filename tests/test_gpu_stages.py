@@ -192,6 +192,36 @@ def test_fused_fit_bit_exact(announce, dtype, dims, n, kq, kk, iters):
         assert np.array_equal(off.cpu().numpy(), roff)
 
 
+def _near_degenerate_centres(g, k, dims, rel):
+    """k centres within ~rel (relative) of one point, plus a few well-separated ones."""
+    base = torch.randn(1, dims, generator=g) * 3
+    cent = base + rel * base.norm() * torch.randn(k, dims, generator=g) / dims ** 0.5
+    cent[-4:] = torch.randn(4, dims, generator=g) * 6
+    return cent
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dims,k", [(128, 64), (64, 100)])
+def test_assign_saturated_candidate_lists(announce, dtype, dims, k):
+    """Centres closer together than the screen's error bound: every token near them is
+    flagged with a saturated candidate list and takes the all-centre canonical fallback."""
+    g = _gen(dims + k)
+    cent = torch.stack([_near_degenerate_centres(g, k, dims, 1e-6) for _ in range(2)])
+    x = (cent[:, :1] + torch.randn(2, 1500, dims, generator=g) * 2).to(dtype)
+    announce(f"{dtype} D={dims} K={k}")
+    if dtype == torch.float32:
+        labels = torch.empty(2, 1500, dtype=torch.int32, device=DEV)
+        norms = torch.empty(2, k, device=DEV)
+        clustering_cuda.assign_tokens_to_centers(x.to(DEV), cent.to(DEV), labels, torch.empty(1, device=DEV), norms,
+                                                 1024)
+    else:
+        labels = clustering_cuda.kmeans_fit([clustering_cuda.KMeansProblem(x.to(DEV), cent.to(DEV))], 1)[0][0]
+    ref = canonical.assign(x.float().numpy(), cent.numpy(), canonical.center_norms(cent.numpy()))
+    # The near-degenerate group really competes: most tokens pick one of its centres.
+    assert (ref < k - 4).mean() > 0.5
+    assert np.array_equal(labels.cpu().numpy(), ref)
+
+
 def test_fit_token_clusters_api(announce):
     g = _gen(77)
     x = _mixture(g, 2, 1000, 128, 8).to(torch.bfloat16)
