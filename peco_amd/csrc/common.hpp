@@ -39,11 +39,13 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
 }
 
 // fp32 -> bf16 with round-to-nearest-even (NaN kept quiet).
+// Round to nearest even; a NaN stays a (quiet) NaN. Written without branches so that
+// unrolled conversions stay straight-line code.
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return static_cast<uint16_t>((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return static_cast<uint16_t>(u >> 16);
+    const uint32_t u = __float_as_uint(f);
+    const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    const uint32_t quiet = (u >> 16) | 0x40u;
+    return static_cast<uint16_t>(f != f ? quiet : rounded);
 }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {

@@ -13,10 +13,10 @@
 // (x itself is split the same way when it is not bf16), whose error against the canonical
 // distance is bounded a priori (|c - c_hi - c_lo| <= 2^-16 |c|, products exact in fp32,
 // fp32 accumulation error <= gamma_n, canonical chain error <= gamma_D). Each token keeps
-// its four smallest screened values with the centre index packed into the low mantissa
+// its three smallest screened values with the centre index packed into the low mantissa
 // bits. With best and second best b1 <= b2 and the bound E, b2 - b1 > 2E proves that the
 // centre of b1 is the canonical argmin. Otherwise every centre screening within b1 + 2E is
-// a candidate (all of them are among the kept four unless that list is saturated); the
+// a candidate (all of them are among the kept three unless that list is saturated); the
 // candidates get the canonical fp32 distance in-kernel, lowest index on ties, and a
 // saturated list falls back to evaluating all centres. Labels are therefore identical to the
 // canonical fixed-order fp32 definition, not approximately equal.
@@ -50,8 +50,11 @@ struct KmProblem {
     int32_t* tile_hist;     // [batch, sort tiles, K]
     float* sums;            // nullable [batch, K, D]: per-cluster sums of the last update
     int batch, tokens, clusters;
-    int assign_begin;       // first linear assign block (batch * ceil(tokens/256) blocks)
-    int update_begin;       // first linear update block (batch * K blocks)
+    int assign_begin;       // first linear assign block of this problem
+    int assign_blocks;      // batch * ceil(tokens / 256)
+    int update_begin;       // first linear prep block (batch * K blocks)
+    int scan_begin;         // first linear update workgroup (batch * ceil(K / 8))
+    int scan_blocks;
     int sort_tiles;
 };
 
@@ -63,6 +66,7 @@ struct KmArgs {
     int num;
     int total_assign_blocks;
     int total_update_blocks;
+    int total_scan_blocks;
     float kappa;      // bound coefficient: |screened - canonical| <= kappa*|x||c| + rounding terms
     float gamma_acc;  // gamma of the MFMA accumulation length (applied to the norm term)
 };
@@ -70,6 +74,7 @@ struct KmArgs {
 struct KmIter {
     const float* src[kMaxKm];  // centres used by this iteration
     float* dst[kMaxKm];        // means written by this iteration
+    int hist;                  // assign adds its labels to the sort tile histograms
 };
 
 namespace {
@@ -77,10 +82,17 @@ namespace {
 __device__ __forceinline__ int km_problem(const KmArgs& a, int block, bool assign) {
     int p = 0;
     if (assign) {
-        while (p + 1 < a.num && block >= a.p[p + 1].assign_begin) ++p;
+        // Assign blocks are laid out largest-K problem first (longest blocks dispatched first).
+        while (p + 1 < a.num && !(block >= a.p[p].assign_begin && block < a.p[p].assign_begin + a.p[p].assign_blocks)) ++p;
     } else {
         while (p + 1 < a.num && block >= a.p[p + 1].update_begin) ++p;
     }
+    return p;
+}
+
+__device__ __forceinline__ int km_scan_problem(const KmArgs& a, int block) {
+    int p = 0;
+    while (p + 1 < a.num && !(block >= a.p[p].scan_begin && block < a.p[p].scan_begin + a.p[p].scan_blocks)) ++p;
     return p;
 }
 
@@ -122,48 +134,64 @@ __global__ __launch_bounds__(64) void km_prep_kernel(KmArgs a, KmIter it) {
     }
     __syncthreads();
     if (threadIdx.x == 0) P.norms[local] = canonical_norm_lds(row, D);
-    // Clear this problem's tile histograms (strided over the problem's blocks).
+    // Clear this problem's tile histograms (strided over the problem's blocks), when it has them.
+    if (!P.tile_hist) return;
     const int64_t hist = static_cast<int64_t>(P.batch) * P.sort_tiles * P.clusters;
     const int64_t nblocks = static_cast<int64_t>(P.batch) * P.clusters;
     for (int64_t i = static_cast<int64_t>(local) * kWave + threadIdx.x; i < hist; i += nblocks * kWave)
         P.tile_hist[i] = 0;
 }
 
-// x operand (B of the MFMA): 8 consecutive channels of one token as bf16 (hi, and lo when split).
+// x operand (B of the MFMA): 8 consecutive channels of one token. bf16 rows are loaded raw
+// first, so every row load of a tile is in flight before any of them is used.
+template <int DT> struct XChunk { u16x8 u; };
+
 template <int DT>
-__device__ __forceinline__ void load_x8(const void* x, int64_t e, bool valid, u16x8& hi, u16x8& lo, float& sq) {
+__device__ __forceinline__ XChunk<DT> load_x8(const void* x, int64_t e) {
+    return XChunk<DT>{*reinterpret_cast<const u16x8*>(static_cast<const uint16_t*>(x) + e)};
+}
+
+// fp16/fp32 rows: load and split one chunk (hi, lo) in place; zero for an invalid token.
+template <int DT>
+__device__ __forceinline__ void load_split_x8(const void* x, int64_t e, bool valid, u16x8& hi, u16x8& lo, float& sq) {
     if (!valid) {
         hi = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
         lo = hi;
         return;
     }
-    if constexpr (DT == kBF16) {
-        hi = *reinterpret_cast<const u16x8*>(static_cast<const uint16_t*>(x) + e);
+    float f[8];
+    if constexpr (DT == kF32) {
+        const f32x4 a = reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + e)[0];
+        const f32x4 b = reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + e)[1];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float f = bf16_bits_to_f32(hi[i]);
-            sq = fmaf(f, f, sq);
-        }
+        for (int i = 0; i < 4; ++i) { f[i] = a[i]; f[4 + i] = b[i]; }
     } else {
-        float f[8];
-        if constexpr (DT == kF32) {
-            const f32x4 a = reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + e)[0];
-            const f32x4 b = reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + e)[1];
+        const u16x8 u = *reinterpret_cast<const u16x8*>(static_cast<const uint16_t*>(x) + e);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) { f[i] = a[i]; f[4 + i] = b[i]; }
-        } else {
-            const u16x8 u = *reinterpret_cast<const u16x8*>(static_cast<const uint16_t*>(x) + e);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) f[i] = f16_bits_to_f32(u[i]);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint16_t h = f32_to_bf16_bits(f[i]);
-            hi[i] = h;
-            lo[i] = f32_to_bf16_bits(f[i] - bf16_bits_to_f32(h));
-            sq = fmaf(f[i], f[i], sq);
-        }
+        for (int i = 0; i < 8; ++i) f[i] = f16_bits_to_f32(u[i]);
     }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint16_t h = f32_to_bf16_bits(f[i]);
+        hi[i] = h;
+        lo[i] = f32_to_bf16_bits(f[i] - bf16_bits_to_f32(h));
+        sq = fmaf(f[i], f[i], sq);
+    }
+}
+
+// bf16 rows: hi of a raw chunk (lo is zero), zero for an invalid token; adds its squares to sq.
+template <int DT>
+__device__ __forceinline__ void split_x8(const XChunk<DT>& r, bool valid, u16x8& hi, u16x8& lo, float& sq) {
+    static_assert(DT == kBF16, "split_x8 handles bf16 rows");
+    float part = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float f = bf16_bits_to_f32(r.u[i]);
+        hi[i] = valid ? r.u[i] : 0;
+        lo[i] = 0;
+        part = fmaf(f, f, part);
+    }
+    sq += valid ? part : 0.0f;
 }
 
 // Assign: one workgroup = 256 tokens of one (problem, batch); wave w owns tokens
@@ -173,6 +201,8 @@ __device__ __forceinline__ void load_x8(const void* x, int64_t e, bool valid, u1
 // lane l holds token l%32 of each column block and centres 8*(i/4)+4*(l/32)+i%4.
 // Screened distance of centres past K (finite, so index bits can be packed into it).
 constexpr float kFarAway = 1.0e37f;
+// Screened values kept per token and lane half (candidates for the canonical recheck).
+constexpr int kTop = 3;
 
 template <int D> struct AssignTiles {
     static constexpr int kRow = D + 8;                 // padded LDS row (16-bit elements)
@@ -276,48 +306,67 @@ __global__ __launch_bounds__(256, 2) void km_assign_kernel(KmArgs a, KmIter it) 
 
     CentreRegs<D> regs;
     load_centres<D>(regs, hi_base, lo_base, norms, 0, K, tid);
+    float nmax = tid < K ? norms[tid] : 0.0f;
+
+    // x row loads are issued before any is used (a token past the end reads the last row and
+    // is masked to zero): both 32-token chunks at once for bf16 input, one chunk at a time
+    // when x is split (fp16/fp32), whose raw and split chunks would not fit in registers together.
+    int tok[2];
+    bool valid[2];
+    XChunk<DT> raw[2][S];
+    auto issue = [&](int c) {
+        tok[c] = tile * kAssignTile + wave * 64 + 32 * c + (lane % 32);
+        valid[c] = tok[c] < P.tokens;
+        const int64_t xrow = static_cast<int64_t>(b) * P.x_stride + static_cast<int64_t>(min(tok[c], P.tokens - 1)) * D;
+#pragma unroll
+        for (int s = 0; s < S; ++s) raw[c][s] = load_x8<DT>(P.x, xrow + 16 * s + 8 * h);
+    };
+    if constexpr (!kSplitX) {
+        issue(0);
+        issue(1);
+    }
 
     // Largest centre norm of this batch entry (for the error bound).
-    float nmax = 0.0f;
-    for (int j = tid; j < K; j += blockDim.x) nmax = fmaxf(nmax, norms[j]);
+    for (int j = tid + blockDim.x; j < K; j += blockDim.x) nmax = fmaxf(nmax, norms[j]);
 #pragma unroll
     for (int m = 1; m < kWave; m <<= 1) nmax = fmaxf(nmax, __shfl_xor(nmax, m, kWave));
     if (lane == 0) red[wave] = nmax;
 
-    int tok[2];
-    bool valid[2];
     u16x8 xh[2][S], xl[2][S];
     float sq[2] = {0.0f, 0.0f};
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-        tok[c] = tile * kAssignTile + wave * 64 + 32 * c + (lane % 32);
-        valid[c] = tok[c] < P.tokens;
-        const int64_t xrow = static_cast<int64_t>(b) * P.x_stride + static_cast<int64_t>(tok[c]) * D;
+        if constexpr (kSplitX) {
+            tok[c] = tile * kAssignTile + wave * 64 + 32 * c + (lane % 32);
+            valid[c] = tok[c] < P.tokens;
+            const int64_t xrow =
+                static_cast<int64_t>(b) * P.x_stride + static_cast<int64_t>(min(tok[c], P.tokens - 1)) * D;
 #pragma unroll
-        for (int s = 0; s < S; ++s) load_x8<DT>(P.x, xrow + 16 * s + 8 * h, valid[c], xh[c][s], xl[c][s], sq[c]);
+            for (int s = 0; s < S; ++s) load_split_x8<DT>(P.x, xrow + 16 * s + 8 * h, valid[c], xh[c][s], xl[c][s], sq[c]);
+        } else {
+#pragma unroll
+            for (int s = 0; s < S; ++s) split_x8<DT>(raw[c][s], valid[c], xh[c][s], xl[c][s], sq[c]);
+        }
         sq[c] += __shfl_xor(sq[c], 32, kWave);
     }
     store_centres<D>(regs, chi[0], clo[0], cn[0], tid);
     __syncthreads();
     nmax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 
-    // Sorted four smallest screened values per token (t[0] <= ... <= t[3]). The centre index
+    // Sorted kTop smallest screened values per token and lane half (t[0] <= t[1] <= ...). The centre index
     // j is packed into the low `ibits` mantissa bits, so min/med3 track value and index
     // together; the packing error is part of the certification bound below.
     const int ibits = 32 - __builtin_clz(static_cast<unsigned>(max(K - 1, 1)));
     const uint32_t imask = (1u << ibits) - 1u;
-    float t[2][4];
+    float t[2][kTop];
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
-        for (int k = 0; k < 4; ++k) t[c][k] = kFarAway;
+        for (int k = 0; k < kTop; ++k) t[c][k] = kFarAway;
     const int nblocks = static_cast<int>(ceil_div(K, 32));
-    for (int blk = 0; blk < nblocks; ++blk) {
-        const int buf = blk & 1;
-        const bool more = blk + 1 < nblocks;
-        if (more) load_centres<D>(regs, hi_base, lo_base, norms, (blk + 1) * 32, K, tid);
-        // Accumulators start at the centre norms: acc = |c|^2 - 2 x.c after the chain.
-        f32x16 acc[2];
+    // MFMA screen of the block in LDS buffer `buf`. Accumulators start at the centre norms:
+    // acc = |c|^2 - 2 x.c after the chain.
+    auto screen = [&](int buf, f32x16 (&acc)[2]) {
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -340,6 +389,9 @@ __global__ __launch_bounds__(256, 2) void km_assign_kernel(KmArgs a, KmIter it) 
                     acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, as_bf16x8(xl[c][s]), acc[c], 0, 0, 0);
             }
         }
+    };
+    // Top-kTop tracking of block blk's screened values.
+    auto track = [&](int blk, const f32x16 (&acc)[2]) {
         const int cb = blk * 32;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -347,14 +399,48 @@ __global__ __launch_bounds__(256, 2) void km_assign_kernel(KmArgs a, KmIter it) 
 #pragma unroll
             for (int c = 0; c < 2; ++c) {
                 const float v = __uint_as_float((__float_as_uint(acc[c][i]) & ~imask) | j);
-                t[c][3] = __builtin_amdgcn_fmed3f(t[c][2], v, t[c][3]);
-                t[c][2] = __builtin_amdgcn_fmed3f(t[c][1], v, t[c][2]);
-                t[c][1] = __builtin_amdgcn_fmed3f(t[c][0], v, t[c][1]);
+#pragma unroll
+                for (int k = kTop - 1; k > 0; --k) t[c][k] = __builtin_amdgcn_fmed3f(t[c][k - 1], v, t[c][k]);
                 t[c][0] = fminf(t[c][0], v);
             }
         }
-        if (more) store_centres<D>(regs, chi[buf ^ 1], clo[buf ^ 1], cn[buf ^ 1], tid);
-        __syncthreads();
+    };
+    // Software pipeline over centre blocks: the MFMAs of block blk+1 are issued before the
+    // VALU tracking of block blk, so the two overlap. Block b sits in LDS buffer b & 1; block
+    // blk+2 is fetched into registers and stored into the buffer block blk has left.
+    auto step = [&](int blk, const f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
+        const bool has1 = blk + 1 < nblocks, has2 = blk + 2 < nblocks;
+        if (has2) load_centres<D>(regs, hi_base, lo_base, norms, (blk + 2) * 32, K, tid);
+        if (has1) screen((blk + 1) & 1, nxt);
+        track(blk, cur);
+        if (has2) store_centres<D>(regs, chi[blk & 1], clo[blk & 1], cn[blk & 1], tid);
+        if (has1) __syncthreads();
+    };
+    // With split x (fp16/fp32 input) at D = 128 the second accumulator set does not fit in
+    // registers; those fits keep one set and screen, then track, each block in turn.
+    constexpr bool kPipelined = !(kSplitX && D > 64);
+    f32x16 acc_a[2];
+    if constexpr (kPipelined) {
+        f32x16 acc_b[2];
+        if (nblocks > 1) load_centres<D>(regs, hi_base, lo_base, norms, 32, K, tid);
+        screen(0, acc_a);
+        if (nblocks > 1) {
+            store_centres<D>(regs, chi[1], clo[1], cn[1], tid);
+            __syncthreads();
+        }
+        for (int blk = 0; blk < nblocks; blk += 2) {
+            step(blk, acc_a, acc_b);
+            if (blk + 1 < nblocks) step(blk + 1, acc_b, acc_a);
+        }
+    } else {
+        for (int blk = 0; blk < nblocks; ++blk) {
+            const bool more = blk + 1 < nblocks;
+            if (more) load_centres<D>(regs, hi_base, lo_base, norms, (blk + 1) * 32, K, tid);
+            screen(blk & 1, acc_a);
+            track(blk, acc_a);
+            if (more) store_centres<D>(regs, chi[(blk + 1) & 1], clo[(blk + 1) & 1], cn[(blk + 1) & 1], tid);
+            __syncthreads();
+        }
     }
 
     const float cmax = sqrtf(nmax) * 1.001f;
@@ -364,9 +450,9 @@ __global__ __launch_bounds__(256, 2) void km_assign_kernel(KmArgs a, KmIter it) 
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
         // The two lane halves of a token hold disjoint centres; combine their lists.
-        float pt[4];
+        float pt[kTop];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) pt[k] = __shfl_xor(t[c][k], 32, kWave);
+        for (int k = 0; k < kTop; ++k) pt[k] = __shfl_xor(t[c][k], 32, kWave);
         const float best = fminf(t[c][0], pt[0]);
         const float second = fminf(fmaxf(t[c][0], pt[0]), fminf(t[c][1], pt[1]));
         int label = static_cast<int>(__float_as_uint(best) & imask);
@@ -378,14 +464,14 @@ __global__ __launch_bounds__(256, 2) void km_assign_kernel(KmArgs a, KmIter it) 
                           (4.0f * 5.9604645e-8f + pack_rel) * (fabsf(best) + fabsf(second)) + 1e-30f;
         const bool flagged = valid[c] && !((second - best) > thr);
         // Every centre that can still be the canonical argmin screens within `bound`. If a
-        // lane's four smallest all fall inside, its list may have missed one (saturated).
+        // lane half's kTop smallest all fall inside, its list may have missed one (saturated).
         const float bound = best + thr;
-        const bool saturated = flagged && (t[c][3] <= bound || pt[3] <= bound);
+        const bool saturated = flagged && (t[c][kTop - 1] <= bound || pt[kTop - 1] <= bound);
         const int64_t trow = static_cast<int64_t>(b) * P.x_stride + static_cast<int64_t>(tok[c]) * D;
         uint64_t key = ~0ull;
         if (flagged && !saturated) {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
+            for (int k = 0; k < kTop; ++k) {
                 if (t[c][k] <= bound) {
                     const int j = static_cast<int>(__float_as_uint(t[c][k]) & imask);
                     const float dist = fmaf(-2.0f, canonical_dot<DT, D>(P.x, trow, cent + static_cast<int64_t>(j) * D),
@@ -424,7 +510,8 @@ __global__ __launch_bounds__(256, 2) void km_assign_kernel(KmArgs a, KmIter it) 
         }
         if (valid[c] && h == 0) {
             P.labels[static_cast<int64_t>(b) * P.tokens + tok[c]] = label;
-            atomicAdd(P.tile_hist + (static_cast<int64_t>(b) * P.sort_tiles + tok[c] / kSortTile) * K + label, 1);
+            if (it.hist)
+                atomicAdd(P.tile_hist + (static_cast<int64_t>(b) * P.sort_tiles + tok[c] / kSortTile) * K + label, 1);
         }
     }
 }
@@ -442,9 +529,35 @@ __device__ __forceinline__ void load_pair(const void* x, int64_t e, float (&v)[P
     }
 }
 
-// Update: one wavefront per (problem, batch, cluster). Sums member rows in original token
-// order (the sorted member list is stable), divides by the count, and prepares the next
-// iteration's split centres and canonical norm.
+// Adds the rows of cnt (1..64) members to s in member order; lane u of `mine` holds the
+// u-th member's token. The batch is rounded up to 16, 32 or 64 loads (the extra ones re-read
+// the last member's row) so every row load is in flight before the first add.
+template <int DT, int PER, int N>
+__device__ __forceinline__ void add_member_batch(const void* x, int64_t xbase, int mine, int cnt, float (&s)[PER]) {
+    constexpr int D = PER * kWave;
+    float v[N][PER];
+#pragma unroll
+    for (int u = 0; u < N; ++u) {
+        const int t = __builtin_amdgcn_readlane(mine, u < cnt ? u : cnt - 1);
+        load_pair<DT, PER>(x, xbase + static_cast<int64_t>(t) * D, v[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < N; ++u)
+        if (u < cnt)
+#pragma unroll
+            for (int i = 0; i < PER; ++i) s[i] = s[i] + v[u][i];
+}
+
+template <int DT, int PER>
+__device__ __forceinline__ void add_members(const void* x, int64_t xbase, int mine, int cnt, float (&s)[PER]) {
+    if (cnt > 32) add_member_batch<DT, PER, 64>(x, xbase, mine, cnt, s);
+    else if (cnt > 16) add_member_batch<DT, PER, 32>(x, xbase, mine, cnt, s);
+    else add_member_batch<DT, PER, 16>(x, xbase, mine, cnt, s);
+}
+
+// Update of a fit: one wavefront per (problem, batch, cluster). Sums member rows in original
+// token order (the sorted member list is stable), divides by the count, and prepares the
+// next iteration's split centres and canonical norm.
 template <int DT, int D>
 __global__ __launch_bounds__(64) void km_update_kernel(KmArgs a, KmIter it) {
     constexpr int PER = D / kWave;  // channels per lane (1 or 2)
@@ -463,45 +576,11 @@ __global__ __launch_bounds__(64) void km_update_kernel(KmArgs a, KmIter it) {
     float s[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) s[i] = 0.0f;
-    // Member indices arrive 64 at a time (one per lane) and are broadcast with readlane; all
-    // of a chunk's row loads (32 bits per lane) are in flight before the adds, which stay in
-    // member (= token) order.
+    // Member indices arrive 64 at a time (one per lane) and are broadcast with readlane.
     for (int m0 = begin; m0 < end; m0 += kWave) {
         const int cnt = min(kWave, end - m0);
-        const int mine = lane < cnt ? idx[m0 + lane] : idx[m0];
-        if (cnt == kWave) {
-            float v[kWave][PER];
-#pragma unroll
-            for (int u = 0; u < kWave; ++u) {
-                const int t = __builtin_amdgcn_readlane(mine, u);
-                load_pair<DT, PER>(P.x, xbase + static_cast<int64_t>(t) * D, v[u]);
-            }
-#pragma unroll
-            for (int u = 0; u < kWave; ++u)
-#pragma unroll
-                for (int i = 0; i < PER; ++i) s[i] = s[i] + v[u][i];
-        } else {
-            int j = 0;
-            for (; j + 16 <= cnt; j += 16) {
-                float v[16][PER];
-#pragma unroll
-                for (int u = 0; u < 16; ++u) {
-                    const int t = __builtin_amdgcn_readlane(mine, j + u);
-                    load_pair<DT, PER>(P.x, xbase + static_cast<int64_t>(t) * D, v[u]);
-                }
-#pragma unroll
-                for (int u = 0; u < 16; ++u)
-#pragma unroll
-                    for (int i = 0; i < PER; ++i) s[i] = s[i] + v[u][i];
-            }
-            for (; j < cnt; ++j) {
-                const int t = __builtin_amdgcn_readlane(mine, j);
-                float v[PER];
-                load_pair<DT, PER>(P.x, xbase + static_cast<int64_t>(t) * D, v);
-#pragma unroll
-                for (int i = 0; i < PER; ++i) s[i] = s[i] + v[i];
-            }
-        }
+        const int mine = idx[m0 + (lane < cnt ? lane : 0)];
+        add_members<DT, PER>(P.x, xbase, mine, cnt, s);
     }
     const int count = end - begin;
     const int64_t cbase = static_cast<int64_t>(local) * D + lane * PER;
@@ -518,6 +597,108 @@ __global__ __launch_bounds__(64) void km_update_kernel(KmArgs a, KmIter it) {
     }
     __syncthreads();
     if (lane == 0) P.norms[local] = canonical_norm_lds(row, D);
+}
+
+constexpr int kScanWaves = 8;     // clusters per update workgroup (one per wavefront)
+constexpr int kScanTile = 4096;   // labels staged in LDS per step (a multiple of 256)
+constexpr int kScanStep = 4 * kWave;  // labels examined per scan step (four per lane)
+constexpr int kRing = 512;        // per-wave member ring (> 64 + kScanStep)
+
+// Update without a sorted member list (peco_recompute_cluster_centers): one wavefront per
+// (problem, batch, cluster), kScanWaves clusters per workgroup. The batch entry's labels stream through LDS in tiles (padded with -1 to whole steps).
+// Each scan step a lane reads four consecutive labels; four ballots find the wave's members
+// and their rank in token order (mbcnt over the four masks plus the lane's own earlier
+// matches). Members enter a ring in token order and are summed 64 at a time, so the sum is
+// the token-order fp32 sum without a sorted member list. The epilogue writes the mean
+// (the previous centre when empty), count, optional sums, and the next iteration's split
+// centres and canonical norm (the last two skipped when their buffers are null).
+template <int DT, int D>
+__global__ __launch_bounds__(kScanWaves * kWave) void km_update_scan_kernel(KmArgs a, KmIter it) {
+    constexpr int PER = D / kWave;  // channels per lane (1 or 2)
+    __shared__ __align__(16) int32_t lab[kScanTile];
+    __shared__ int32_t ring[kScanWaves][kRing];
+    __shared__ float row[kScanWaves][D];
+    const int p = km_scan_problem(a, blockIdx.x);
+    const KmProblem& P = a.p[p];
+    const int K = P.clusters;
+    const int groups = static_cast<int>(ceil_div(K, kScanWaves));
+    const int local = blockIdx.x - P.scan_begin;
+    const int b = local / groups;
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int j = (local % groups) * kScanWaves + wave;
+    const bool active = j < K;
+    const int32_t* labels = P.labels + static_cast<int64_t>(b) * P.tokens;
+    const int64_t xbase = static_cast<int64_t>(b) * P.x_stride + lane * PER;
+    int32_t* q = ring[wave];
+    float s[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) s[i] = 0.0f;
+    int count = 0, head = 0, tail = 0;  // ring positions (wave-uniform, never wrapped)
+    // Sums the `cnt` members at the ring head.
+    auto drain = [&](int cnt) {
+        // The ring writes precede this read in the wave's program order (LDS is in order).
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int mine = q[(head + (lane < cnt ? lane : 0)) & (kRing - 1)];
+        add_members<DT, PER>(P.x, xbase, mine, cnt, s);
+        __builtin_amdgcn_wave_barrier();  // ring slots are rewritten only after `mine` is read
+        head += cnt;
+    };
+    for (int t0 = 0; t0 < P.tokens; t0 += kScanTile) {
+        const int n = min(kScanTile, P.tokens - t0);
+        const int padded = static_cast<int>(ceil_div(n, kScanStep)) * kScanStep;
+        __syncthreads();  // the previous tile is fully scanned
+        for (int i = threadIdx.x; i < padded; i += blockDim.x) lab[i] = i < n ? labels[t0 + i] : -1;
+        __syncthreads();
+        if (!active) continue;
+        for (int c0 = 0; c0 < padded; c0 += kScanStep) {
+            const int4 L = *reinterpret_cast<const int4*>(&lab[c0 + 4 * lane]);
+            const bool e0 = L.x == j, e1 = L.y == j, e2 = L.z == j, e3 = L.w == j;
+            const uint64_t m0 = __ballot(e0), m1 = __ballot(e1), m2 = __ballot(e2), m3 = __ballot(e3);
+            if ((m0 | m1 | m2 | m3) == 0) continue;
+            // Members of lower lanes (all four slots) come first, then this lane's own.
+            int r = tail + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m0 >> 32),
+                                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m0), 0));
+            r += __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m1 >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m1), 0));
+            r += __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m2 >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m2), 0));
+            r += __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m3 >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m3), 0));
+            const int tok = t0 + c0 + 4 * lane;
+            if (e0) q[r & (kRing - 1)] = tok;
+            r += e0;
+            if (e1) q[r & (kRing - 1)] = tok + 1;
+            r += e1;
+            if (e2) q[r & (kRing - 1)] = tok + 2;
+            r += e2;
+            if (e3) q[r & (kRing - 1)] = tok + 3;
+            const int add = __popcll(m0) + __popcll(m1) + __popcll(m2) + __popcll(m3);
+            tail += add;
+            count += add;
+            while (tail - head >= kWave) drain(kWave);
+        }
+    }
+    if (!active) return;
+    if (tail > head) drain(tail - head);
+    const int64_t cl = static_cast<int64_t>(b) * K + j;
+    const int64_t cbase = cl * D + lane * PER;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const float mean = count > 0 ? s[i] / static_cast<float>(count) : it.src[p][cbase + i];
+        it.dst[p][cbase + i] = mean;
+        if (P.sums) P.sums[cbase + i] = s[i];
+        row[wave][lane * PER + i] = mean;
+        if (P.prep_hi) {
+            uint16_t hi, lo;
+            split_neg2(mean, hi, lo);
+            P.prep_hi[cbase + i] = hi;
+            P.prep_lo[cbase + i] = lo;
+        }
+    }
+    if (lane == 0 && P.counts) P.counts[cl] = count;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane == 0 && P.norms) P.norms[cl] = canonical_norm_lds(row[wave], D);
 }
 
 template <int DT, int D>
@@ -611,10 +792,11 @@ hipError_t km_fit(const KmFitDesc* descs, int num, int dims, int dtype, int iter
         P.tokens = d.tokens;
         P.clusters = d.clusters;
         P.sort_tiles = sort_tiles(d.tokens);
-        P.assign_begin = ab;
+        P.assign_blocks = d.batch * static_cast<int>(ceil_div(d.tokens, kAssignTile));
         P.update_begin = ub;
-        ab += d.batch * static_cast<int>(ceil_div(d.tokens, kAssignTile));
+        ab += P.assign_blocks;
         ub += d.batch * d.clusters;
+        P.scan_blocks = d.batch * static_cast<int>(ceil_div(d.clusters, kScanWaves));
         SortProblem& q = sa.p[i];
         q.labels = d.labels;
         q.indices = d.indices;
@@ -628,6 +810,20 @@ hipError_t km_fit(const KmFitDesc* descs, int num, int dims, int dtype, int iter
     }
     a.total_assign_blocks = ab;
     a.total_update_blocks = ub;
+    // Longest workgroups first: assign blocks of the problem with more centres, update
+    // workgroups of the problem with fewer centres (more members per cluster).
+    {
+        int order[kMaxKm] = {0, 1};
+        if (num == 2 && a.p[1].clusters > a.p[0].clusters) std::swap(order[0], order[1]);
+        int begin = 0, scan = 0;
+        for (int i = 0; i < num; ++i) {
+            a.p[order[i]].assign_begin = begin;
+            begin += a.p[order[i]].assign_blocks;
+            a.p[order[num - 1 - i]].scan_begin = scan;
+            scan += a.p[order[num - 1 - i]].scan_blocks;
+        }
+        a.total_scan_blocks = scan;
+    }
     a.kappa = km_kappa(dtype, dims);
     a.gamma_acc = static_cast<float>(gamma_n(3.0 * dims + 2));
     sort_args_finalize(sa);
@@ -638,6 +834,7 @@ hipError_t km_fit(const KmFitDesc* descs, int num, int dims, int dtype, int iter
             iters[i].dst[q] = dst;
             iters[i].src[q] = i == 0 ? a.p[q].centers_in : iters[i - 1].dst[q];
         }
+        iters[i].hist = 1;
     }
 #define PECO_FIT(DT_, D_) return run_fit<DT_, D_>(a, iters.data(), iterations, sa, stream)
     if (dims == 128) {
@@ -708,9 +905,8 @@ PECO_API int peco_assign_tokens_to_centers(const float* x, const float* centers,
     a.num = 1;
     KmProblem& P = a.p[0];
     const size_t bkd = static_cast<size_t>(batch) * clusters * dims;
-    const size_t hist = sort_workspace_ints(batch, tokens, clusters);
     void* buf = nullptr;
-    const size_t bytes = bkd * 4 + (center_norms ? 0 : static_cast<size_t>(batch) * clusters * 4) + hist * 4 + 256;
+    const size_t bytes = bkd * 4 + (center_norms ? 0 : static_cast<size_t>(batch) * clusters * 4) + 256;
     hipError_t e = hipMallocAsync(&buf, bytes, s);
     if (e != hipSuccess) return e;
     char* w = static_cast<char*>(buf);
@@ -721,13 +917,13 @@ PECO_API int peco_assign_tokens_to_centers(const float* x, const float* centers,
     w += bkd * 4;
     if (center_norms) P.norms = center_norms;
     else { P.norms = reinterpret_cast<float*>(w); w += static_cast<size_t>(batch) * clusters * 4; }
-    P.tile_hist = reinterpret_cast<int32_t*>(w);
     P.labels = labels;
     P.batch = batch;
     P.tokens = tokens;
     P.clusters = clusters;
     P.sort_tiles = sort_tiles(tokens);
     a.total_assign_blocks = batch * static_cast<int>(ceil_div(tokens, kAssignTile));
+    P.assign_blocks = a.total_assign_blocks;
     a.total_update_blocks = batch * clusters;
     a.kappa = km_kappa(kF32, dims);
     a.gamma_acc = static_cast<float>(gamma_n(3.0 * dims + 2));
@@ -751,61 +947,33 @@ PECO_API int peco_recompute_cluster_centers(const float* x, const int32_t* label
                                             int32_t* counts, float* means, int batch, int tokens, int dims,
                                             int clusters, void* stream) {
     if (!x || !labels || !previous || !counts || !means || batch < 1 || tokens < 1 || clusters < 1 ||
-        clusters > kMaxSortClusters || (dims != 64 && dims != 128))
+        (dims != 64 && dims != 128))
         return kInvalidValue;
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    const size_t bkd = static_cast<size_t>(batch) * clusters * dims;
-    const size_t hist = sort_workspace_ints(batch, tokens, clusters);
-    const size_t idx = static_cast<size_t>(batch) * tokens;
-    const size_t off = static_cast<size_t>(batch) * (clusters + 1);
-    const size_t nrm = static_cast<size_t>(batch) * clusters;
-    void* buf = nullptr;
-    hipError_t e = hipMallocAsync(&buf, (bkd * 2 + hist + idx + off + nrm) * 4 + 256, s);
-    if (e != hipSuccess) return e;
-    char* w = static_cast<char*>(buf);
-    SortArgs sa{};
-    sa.num = 1;
-    SortProblem& q = sa.p[0];
-    q.labels = labels;
-    q.indices = reinterpret_cast<int32_t*>(w);
-    w += idx * 4;
-    q.offsets = reinterpret_cast<int32_t*>(w);
-    w += off * 4;
-    q.tile_hist = reinterpret_cast<int32_t*>(w);
-    w += hist * 4;
-    q.counts = counts;
-    q.ranks = nullptr;
-    q.batch = batch;
-    q.tokens = tokens;
-    q.clusters = clusters;
-    sort_args_finalize(sa);
-    e = launch_cluster_sort(sa, s, true);
-    if (e == hipSuccess) {
-        KmArgs a{};
-        a.num = 1;
-        KmProblem& P = a.p[0];
-        P.x = x;
-        P.x_stride = static_cast<int64_t>(tokens) * dims;
-        P.indices = q.indices;
-        P.offsets = q.offsets;
-        P.prep_hi = reinterpret_cast<uint16_t*>(w);
-        P.prep_lo = P.prep_hi + bkd;
-        w += bkd * 4;
-        P.norms = reinterpret_cast<float*>(w);
-        P.sums = sums;
-        P.batch = batch;
-        P.tokens = tokens;
-        P.clusters = clusters;
-        a.total_update_blocks = batch * clusters;
-        KmIter it{};
-        it.src[0] = previous;
-        it.dst[0] = means;
-        if (dims == 128)
-            hipLaunchKernelGGL((km_update_kernel<kF32, 128>), dim3(a.total_update_blocks), dim3(64), 0, s, a, it);
-        else
-            hipLaunchKernelGGL((km_update_kernel<kF32, 64>), dim3(a.total_update_blocks), dim3(64), 0, s, a, it);
-        e = hipGetLastError();
-    }
-    hipError_t f = hipFreeAsync(buf, s);
-    return e != hipSuccess ? e : f;
+    // Members are found from the labels directly (labels outside [0, clusters) join no
+    // cluster); no sort, no workspace.
+    KmArgs a{};
+    a.num = 1;
+    KmProblem& P = a.p[0];
+    P.x = x;
+    P.x_stride = static_cast<int64_t>(tokens) * dims;
+    P.labels = const_cast<int32_t*>(labels);
+    P.counts = counts;
+    P.sums = sums;
+    P.batch = batch;
+    P.tokens = tokens;
+    P.clusters = clusters;
+    P.scan_begin = 0;
+    P.scan_blocks = batch * static_cast<int>(ceil_div(clusters, kScanWaves));
+    a.total_scan_blocks = P.scan_blocks;
+    KmIter it{};
+    it.src[0] = previous;
+    it.dst[0] = means;
+    if (dims == 128)
+        hipLaunchKernelGGL((km_update_scan_kernel<kF32, 128>), dim3(a.total_scan_blocks), dim3(kScanWaves * kWave), 0,
+                           s, a, it);
+    else
+        hipLaunchKernelGGL((km_update_scan_kernel<kF32, 64>), dim3(a.total_scan_blocks), dim3(kScanWaves * kWave), 0,
+                           s, a, it);
+    return hipGetLastError();
 }
