@@ -2,7 +2,7 @@
 //
 // The permutation is the stable argsort of labels per batch entry
 // (peco/clustering.py:105, torch.argsort(..., stable=True)), computed as a counting sort:
-//   1. sort_hist:  per 1024-token tile, a label histogram (LDS atomics; counts only).
+//   1. sort_hist:  per 256-token tile, a label histogram (LDS atomics; counts only).
 //   2. sort_scan:  per batch entry, scan tiles per cluster and clusters -> absolute
 //                  start position of each (tile, cluster) run, counts and offsets.
 //   3. sort_place: per tile, one wavefront ranks 64 tokens per step. Lanes holding the
@@ -87,13 +87,18 @@ __global__ __launch_bounds__(256) void sort_scan_kernel(SortArgs args) {
     const SortProblem& P = args.p[pi];
     const int b = blockIdx.x - P.batch_begin;
     const int K = P.clusters;
-    int32_t* th = P.tile_hist + static_cast<int64_t>(b) * P.tiles * K;
+    const int tiles = P.tiles;
+    int32_t* th = P.tile_hist + static_cast<int64_t>(b) * tiles * K;
+    constexpr int kBatch = 8;  // tile counts in flight per thread
+    // Pass 1 (loads only): total count of each cluster.
     for (int k = threadIdx.x; k < K; k += blockDim.x) {
         int run = 0;
-        for (int tile = 0; tile < P.tiles; ++tile) {
-            const int c = th[static_cast<int64_t>(tile) * K + k];
-            th[static_cast<int64_t>(tile) * K + k] = run;
-            run += c;
+        for (int t0 = 0; t0 < tiles; t0 += kBatch) {
+            int c[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) c[u] = t0 + u < tiles ? th[static_cast<int64_t>(t0 + u) * K + k] : 0;
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) run += c[u];
         }
         cnt[k] = run;
     }
@@ -112,10 +117,26 @@ __global__ __launch_bounds__(256) void sort_scan_kernel(SortArgs args) {
         const int c = cnt[k];
         off[k] = run;
         if (counts) counts[k] = c;
-        for (int tile = 0; tile < P.tiles; ++tile) th[static_cast<int64_t>(tile) * K + k] += run;
+        cnt[k] = run;  // becomes the cluster's first sorted position
         run += c;
     }
     if (threadIdx.x == 0) off[K] = total;
+    __syncthreads();
+    // Pass 2: each (tile, cluster) count becomes the absolute start of that run. A batch of
+    // counts is read before any of it is overwritten.
+    for (int k = threadIdx.x; k < K; k += blockDim.x) {
+        int pos = cnt[k];
+        for (int t0 = 0; t0 < tiles; t0 += kBatch) {
+            int c[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) c[u] = t0 + u < tiles ? th[static_cast<int64_t>(t0 + u) * K + k] : 0;
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                if (t0 + u < tiles) th[static_cast<int64_t>(t0 + u) * K + k] = pos;
+                pos += c[u];
+            }
+        }
+    }
 }
 
 __global__ __launch_bounds__(64) void sort_place_kernel(SortArgs args) {
@@ -129,9 +150,19 @@ __global__ __launch_bounds__(64) void sort_place_kernel(SortArgs args) {
     const int lane = threadIdx.x;
     const int32_t* th = P.tile_hist + (static_cast<int64_t>(b) * P.tiles + tile) * K;
     int32_t* th_mut = P.tile_hist + (static_cast<int64_t>(b) * P.tiles + tile) * K;
-    for (int k = lane; k < K; k += kWave) {
-        base[k] = th[k];
-        if (args.zero_hist) th_mut[k] = 0;
+    // Run starts of this tile (four loads in flight per lane before any store).
+    for (int k0 = 0; k0 < K; k0 += 4 * kWave) {
+        int v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = k0 + u * kWave + lane < K ? th[k0 + u * kWave + lane] : 0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int k = k0 + u * kWave + lane;
+            if (k < K) {
+                base[k] = v[u];
+                if (args.zero_hist) th_mut[k] = 0;
+            }
+        }
     }
     __syncthreads();
     const int bits = K > 1 ? 32 - __builtin_clz(static_cast<unsigned>(K - 1)) : 0;

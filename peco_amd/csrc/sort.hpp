@@ -5,8 +5,9 @@
 
 namespace peco {
 
-// Tokens per sort tile: one tile is ranked by a single wavefront, 64 tokens per step.
-constexpr int kSortTile = 1024;
+// Tokens per sort tile: one tile is ranked by a single wavefront, 64 tokens per step. It
+// equals the k-means assign tile, so each tile histogram row has a single producer.
+constexpr int kSortTile = 256;
 constexpr int kMaxSortClusters = 16384;
 
 struct SortProblem {
