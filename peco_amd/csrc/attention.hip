@@ -254,16 +254,6 @@ template <int D> struct Tiles {
     static __device__ __forceinline__ int swz_v(int row) { return CH == 16 ? 4 * (row % 4) : 4 * ((row >> 1) & 1); }
 };
 
-// Physical key row of virtual stream row r: the largest cluster c with soff[c] <= r holds it.
-__device__ __forceinline__ int stream_row(const int* soff, const int* kpre, int ck, int r) {
-    int lo = 0, hi = ck - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (soff[mid] <= r) lo = mid;
-        else hi = mid - 1;
-    }
-    return kpre[lo] + (r - soff[lo]);
-}
 
 // Issue the direct-to-LDS loads of one K and one V tile (no wait). Rows past the stream end
 // read row 0 of the head: their K scores are masked to -inf and their P is 0.
@@ -307,8 +297,10 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     __shared__ int prow[2][kKTile];
     __shared__ int tmp[4];
     extern __shared__ int dyn[];
-    int* soff = dyn;            // [ck] stream offset of each key cluster
-    int* kpre = dyn + ck;       // [ck + 1]
+    // Key stream of this query cluster: the kept, non-empty key clusters in order. kst[i] is
+    // the first physical key row of the i-th of them, kof[i] its offset in the stream.
+    int* kst = dyn;             // [ck]
+    int* kof = dyn + ck;        // [ck + 1]
 
     const int bh = blockIdx.x % bhn;
     const int slot = blockIdx.x / bhn;
@@ -318,32 +310,46 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     const int q_start = item[0], qc = item[1], q_rows = item[2];
     const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave, h = lane / 32;
 
-    // Key stream of this query cluster: kept clusters in order, offsets soff.
     const uint8_t* sel = selected + (static_cast<int64_t>(bh) * cq + qc) * ck;
     const int32_t* gk = W.kprefix + static_cast<int64_t>(bh) * (ck + 1);
-    int L;
+    int L, nk;
     {
         const int per = static_cast<int>(ceil_div(ck, 256));
         const int c0 = tid * per, c1 = min(ck, c0 + per);
-        int local = 0;
+        int local = 0, lcount = 0;
         for (int c = c0; c < c1; ++c) {
             const int a = gk[c], e = gk[c + 1];
-            kpre[c] = a;
-            local += sel[c] ? e - a : 0;
+            if (sel[c] && e > a) {
+                local += e - a;
+                ++lcount;
+            }
         }
-        if (tid == 0) kpre[ck] = gk[ck];
         int run = block_scan256(local, tmp, &L);
+        int idx = block_scan256(lcount, tmp, &nk);
         for (int c = c0; c < c1; ++c) {
-            soff[c] = run;
-            run += sel[c] ? gk[c + 1] - gk[c] : 0;
+            const int a = gk[c], e = gk[c + 1];
+            if (sel[c] && e > a) {
+                kst[idx] = a;
+                kof[idx] = run;
+                ++idx;
+                run += e - a;
+            }
         }
+        if (tid == 0) kof[nk] = L;
     }
     __syncthreads();
     const int ntiles = static_cast<int>(ceil_div(L, kKTile));
+    // Physical row of stream row r (r < L). Each of threads 0..63 asks for increasing rows
+    // (its row of every tile), so a forward-only cursor over the kept clusters suffices.
+    int cur = 0;
+    auto row_of = [&](int r) {
+        while (cur + 1 < nk && kof[cur + 1] <= r) ++cur;
+        return kst[cur] + (r - kof[cur]);
+    };
     if (tid < kKTile) {
-        prow[0][tid] = tid < L ? stream_row(soff, kpre, ck, tid) : 0;
+        prow[0][tid] = tid < L ? row_of(tid) : 0;
         const int r1 = kKTile + tid;
-        prow[1][tid] = r1 < L ? stream_row(soff, kpre, ck, r1) : 0;
+        prow[1][tid] = r1 < L ? row_of(r1) : 0;
     }
 
     // Q^T operand: lane holds query row (32*wave + l%32), channels 16s + 8h .. +7.
@@ -393,6 +399,17 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
                     const u16x8 kf = *reinterpret_cast<const u16x8*>(kt + krow * D + pc * 8);
                     sacc[cb] = Mfma<DT>::run(kf, qf[s], sacc[cb]);
                 }
+            }
+            // K-fragment reads run kLook MFMAs ahead of their use (LDS latency > one MFMA).
+            {
+                constexpr int kLook = 4;
+                __builtin_amdgcn_sched_group_barrier(0x100, kLook, 0);  // DS reads
+#pragma unroll
+                for (int i = 0; i < 2 * S - kLook; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, kLook, 0);
             }
 #pragma unroll
             for (int cb = 0; cb < 2; ++cb) {
@@ -456,7 +473,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
         }
         if (more && tid < kKTile) {
             const int r = (tile + 2) * kKTile + tid;
-            prow[buf][tid] = r < L ? stream_row(soff, kpre, ck, r) : 0;
+            prow[buf][tid] = r < L ? row_of(r) : 0;
         }
         __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of the next tile have landed
         __syncthreads();
