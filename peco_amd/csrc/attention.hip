@@ -128,16 +128,40 @@ __global__ __launch_bounds__(256) void build_work_kernel(const uint8_t* __restri
         if (threadIdx.x == 0) qoff[cq] = min(sq, total);
     }
     __syncthreads();
-    // Kept keys per query cluster (one wave per query cluster, lanes over key clusters).
+    // Kept keys per query cluster: one wave per map row, two rows per pass, each row's bytes
+    // read with all of a pass's loads (8 per row and lane) in flight at once.
     {
         const int wave = threadIdx.x / kWave, lane = lane_id();
-        for (int c = wave; c < cq; c += 4) {
-            const uint8_t* row = selected + (static_cast<int64_t>(bh) * cq + c) * ck;
-            int s = 0;
-            for (int kc = lane; kc < ck; kc += kWave) s += row[kc] ? ksz[kc] : 0;
+        constexpr int kU = 8;
+        for (int c0 = wave; c0 < cq; c0 += 8) {
+            int sum[2] = {0, 0};
+            for (int k0 = 0; k0 < ck; k0 += kU * kWave) {
+                uint8_t m[2][kU];
 #pragma unroll
-            for (int m = 1; m < kWave; m <<= 1) s += __shfl_xor(s, m, kWave);
-            if (lane == 0) kept[c] = s;
+                for (int t = 0; t < 2; ++t) {
+                    const int c = c0 + 4 * t;
+                    const uint8_t* row = selected + (static_cast<int64_t>(bh) * cq + min(c, cq - 1)) * ck;
+#pragma unroll
+                    for (int u = 0; u < kU; ++u) {
+                        // Unconditional load (clamped index), masked after: a guarded load
+                        // would wait for each byte before issuing the next.
+                        const int kc = k0 + u * kWave + lane;
+                        const uint8_t v = row[min(kc, ck - 1)];
+                        m[t][u] = (c < cq && kc < ck) ? v : 0;
+                    }
+                }
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int u = 0; u < kU; ++u)
+                        if (m[t][u]) sum[t] += ksz[k0 + u * kWave + lane];
+            }
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+#pragma unroll
+                for (int m = 1; m < kWave; m <<= 1) sum[t] += __shfl_xor(sum[t], m, kWave);
+                if (lane == 0 && c0 + 4 * t < cq) kept[c0 + 4 * t] = sum[t];
+            }
         }
     }
     __syncthreads();

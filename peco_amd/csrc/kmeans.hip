@@ -306,7 +306,8 @@ __global__ __launch_bounds__(256, 2) void km_assign_kernel(KmArgs a, KmIter it) 
 
     CentreRegs<D> regs;
     load_centres<D>(regs, hi_base, lo_base, norms, 0, K, tid);
-    float nmax = tid < K ? norms[tid] : 0.0f;
+    const float n0 = norms[min(tid, K - 1)];
+    float nmax = tid < K ? n0 : 0.0f;
 
     // x row loads are issued before any is used (a token past the end reads the last row and
     // is masked to zero): both 32-token chunks at once for bf16 input, one chunk at a time

@@ -105,7 +105,7 @@ __global__ __launch_bounds__(kSelWaves * kWave) void select_kernel(
 #pragma unroll
         for (int v = 0; v < kSelLoads; ++v) {
             const int t = v * kSelThreads + static_cast<int>(threadIdx.x);
-            if (t < n) staged[v] = src[t];
+            staged[v] = src[min(t, n - 1)];  // unconditional (clamped): all loads in flight
         }
     };
     auto store = [&](int base) {
@@ -129,7 +129,8 @@ __global__ __launch_bounds__(kSelWaves * kWave) void select_kernel(
 #pragma unroll
     for (int e = 0; e < KPL; ++e) {
         const int j = e * kSelBlock + lane;
-        const int w = j < ck ? kcount[j] : 0;
+        const int wl = kcount[min(j, ck - 1)];
+        const int w = j < ck ? wl : 0;
         logit[e] = w > 0 ? logf(static_cast<float>(w)) : -INFINITY;
     }
     fetch(0);

@@ -96,7 +96,11 @@ __global__ __launch_bounds__(256) void sort_scan_kernel(SortArgs args) {
         for (int t0 = 0; t0 < tiles; t0 += kBatch) {
             int c[kBatch];
 #pragma unroll
-            for (int u = 0; u < kBatch; ++u) c[u] = t0 + u < tiles ? th[static_cast<int64_t>(t0 + u) * K + k] : 0;
+            for (int u = 0; u < kBatch; ++u) {
+                // Clamped unconditional loads (masked after) stay in flight together.
+                const int v = th[static_cast<int64_t>(min(t0 + u, tiles - 1)) * K + k];
+                c[u] = t0 + u < tiles ? v : 0;
+            }
 #pragma unroll
             for (int u = 0; u < kBatch; ++u) run += c[u];
         }
@@ -129,7 +133,10 @@ __global__ __launch_bounds__(256) void sort_scan_kernel(SortArgs args) {
         for (int t0 = 0; t0 < tiles; t0 += kBatch) {
             int c[kBatch];
 #pragma unroll
-            for (int u = 0; u < kBatch; ++u) c[u] = t0 + u < tiles ? th[static_cast<int64_t>(t0 + u) * K + k] : 0;
+            for (int u = 0; u < kBatch; ++u) {
+                const int v = th[static_cast<int64_t>(min(t0 + u, tiles - 1)) * K + k];
+                c[u] = t0 + u < tiles ? v : 0;
+            }
 #pragma unroll
             for (int u = 0; u < kBatch; ++u) {
                 if (t0 + u < tiles) th[static_cast<int64_t>(t0 + u) * K + k] = pos;
@@ -154,7 +161,10 @@ __global__ __launch_bounds__(64) void sort_place_kernel(SortArgs args) {
     for (int k0 = 0; k0 < K; k0 += 4 * kWave) {
         int v[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = k0 + u * kWave + lane < K ? th[k0 + u * kWave + lane] : 0;
+        for (int u = 0; u < 4; ++u) {
+            const int x = th[min(k0 + u * kWave + lane, K - 1)];
+            v[u] = k0 + u * kWave + lane < K ? x : 0;
+        }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int k = k0 + u * kWave + lane;
@@ -178,7 +188,8 @@ __global__ __launch_bounds__(64) void sort_place_kernel(SortArgs args) {
 #pragma unroll
     for (int st = 0; st < kSteps; ++st) {
         const int t = begin + st * kWave + lane;
-        labs[st] = t < end ? lab[t] : -1;
+        const int raw = lab[min(t, end - 1)];  // clamped, unconditional: all loads in flight
+        labs[st] = t < end ? raw : -1;
     }
 #pragma unroll
     for (int st = 0; st < kSteps; ++st) {
