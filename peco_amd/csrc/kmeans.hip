@@ -56,6 +56,9 @@ struct KmProblem {
     int scan_begin;         // first linear update workgroup (batch * ceil(K / 8))
     int scan_blocks;
     int sort_tiles;
+    int upd_begin;          // first linear km_update_kernel workgroup of this problem
+    int upd_blocks;
+    int upd_shared;         // 1: one workgroup per cluster, 0: one wavefront per cluster
 };
 
 constexpr int kMaxKm = 2;
@@ -67,6 +70,7 @@ struct KmArgs {
     int total_assign_blocks;
     int total_update_blocks;
     int total_scan_blocks;
+    int total_upd_blocks;
     float kappa;      // bound coefficient: |screened - canonical| <= kappa*|x||c| + rounding terms
     float gamma_acc;  // gamma of the MFMA accumulation length (applied to the norm term)
 };
@@ -530,74 +534,186 @@ __device__ __forceinline__ void load_pair(const void* x, int64_t e, float (&v)[P
     }
 }
 
-// Adds the rows of cnt (1..64) members to s in member order; lane u of `mine` holds the
-// u-th member's token. The batch is rounded up to 16, 32 or 64 loads (the extra ones re-read
-// the last member's row) so every row load is in flight before the first add.
+// Rows of up to N members as loaded: 16-bit inputs keep their raw 32-bit words (two
+// channels per lane) until they are added, so a batch costs N registers per lane.
+template <int DT, int PER, int N> struct MemberRows {
+    static constexpr int W = DT == kF32 ? PER : (PER + 1) / 2;  // 32-bit words per member
+    uint32_t w[N][W];
+};
+
+// Buffer resource over the rows of one batch entry of x: the member row offset goes in the
+// scalar offset of each load (the member index is wave-uniform after readlane) and the lane's
+// channels in the vector offset, so a load needs no per-member address registers.
+struct XRows {
+    __amdgpu_buffer_rsrc_t rsrc;
+    int lane_bytes;  // byte offset of this lane's channels within a row
+};
+
+template <int DT, int D>
+__device__ __forceinline__ XRows x_rows(const void* x, int64_t elem_offset, int tokens, int lane) {
+    constexpr int E = DT == kF32 ? 4 : 2;
+    constexpr int PER = D / kWave;
+    const char* base = static_cast<const char*>(x) + elem_offset * E;
+    const int64_t bytes = static_cast<int64_t>(tokens) * D * E;
+    XRows r;
+    r.rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), 0,
+                                               static_cast<int>(bytes < 0x7fffffff ? bytes : 0x7fffffff), 0x00020000);
+    r.lane_bytes = lane * PER * E;
+    return r;
+}
+
+// Loads the rows of cnt (1..N) members; lane u of `mine` holds the u-th member's token. The
+// batch is rounded up to N loads (the extra ones re-read the last member's row) so every row
+// load is in flight before the first add.
 template <int DT, int PER, int N>
-__device__ __forceinline__ void add_member_batch(const void* x, int64_t xbase, int mine, int cnt, float (&s)[PER]) {
+__device__ __forceinline__ void load_member_rows(const XRows& xr, int mine, int cnt, MemberRows<DT, PER, N>& r) {
     constexpr int D = PER * kWave;
-    float v[N][PER];
+    constexpr int E = DT == kF32 ? 4 : 2;
 #pragma unroll
     for (int u = 0; u < N; ++u) {
         const int t = __builtin_amdgcn_readlane(mine, u < cnt ? u : cnt - 1);
-        load_pair<DT, PER>(x, xbase + static_cast<int64_t>(t) * D, v[u]);
+        const int row = t * (D * E);
+        if constexpr (DT == kF32 && PER == 2) {
+            const auto w = __builtin_amdgcn_raw_buffer_load_b64(xr.rsrc, xr.lane_bytes, row, 0);
+            r.w[u][0] = w[0];
+            r.w[u][1] = w[1];
+        } else if constexpr (DT == kF32 || PER == 2) {
+            r.w[u][0] = __builtin_amdgcn_raw_buffer_load_b32(xr.rsrc, xr.lane_bytes, row, 0);
+        } else {
+            r.w[u][0] = __builtin_amdgcn_raw_buffer_load_b16(xr.rsrc, xr.lane_bytes, row, 0);
+        }
     }
+}
+
+// Adds the first cnt loaded rows to s in member order.
+template <int DT, int PER, int N>
+__device__ __forceinline__ void fold_member_rows(const MemberRows<DT, PER, N>& r, int cnt, float (&s)[PER]) {
+    constexpr int H = DT == kBF16 ? kBF16 : kF16;
 #pragma unroll
     for (int u = 0; u < N; ++u)
-        if (u < cnt)
+        if (u < cnt) {
+            float v[PER];
+            if constexpr (DT == kF32) {
 #pragma unroll
-            for (int i = 0; i < PER; ++i) s[i] = s[i] + v[u][i];
+                for (int i = 0; i < PER; ++i) v[i] = __uint_as_float(r.w[u][i]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < PER; ++i) v[i] = half_to_f32<H>(static_cast<uint16_t>(r.w[u][0] >> (16 * i)));
+            }
+#pragma unroll
+            for (int i = 0; i < PER; ++i) s[i] = s[i] + v[i];
+        }
+}
+
+// Adds the rows of cnt (1..N) members to s in member order.
+template <int DT, int PER, int N>
+__device__ __forceinline__ void add_member_batch(const XRows& xr, int mine, int cnt, float (&s)[PER]) {
+    MemberRows<DT, PER, N> r;
+    load_member_rows<DT, PER, N>(xr, mine, cnt, r);
+    fold_member_rows<DT, PER, N>(r, cnt, s);
 }
 
 template <int DT, int PER>
-__device__ __forceinline__ void add_members(const void* x, int64_t xbase, int mine, int cnt, float (&s)[PER]) {
-    if (cnt > 32) add_member_batch<DT, PER, 64>(x, xbase, mine, cnt, s);
-    else if (cnt > 16) add_member_batch<DT, PER, 32>(x, xbase, mine, cnt, s);
-    else add_member_batch<DT, PER, 16>(x, xbase, mine, cnt, s);
+__device__ __forceinline__ void add_members(const XRows& xr, int mine, int cnt, float (&s)[PER]) {
+    if (cnt > 32) add_member_batch<DT, PER, 64>(xr, mine, cnt, s);
+    else if (cnt > 16) add_member_batch<DT, PER, 32>(xr, mine, cnt, s);
+    else add_member_batch<DT, PER, 16>(xr, mine, cnt, s);
 }
 
-// Update of a fit: one wavefront per (problem, batch, cluster). Sums member rows in original
-// token order (the sorted member list is stable), divides by the count, and prepares the
-// next iteration's split centres and canonical norm.
+// Update of a fit, four wavefronts per workgroup. Sums member rows in original token order
+// (the sorted member list is stable), divides by the count, and prepares the next
+// iteration's split centres and canonical norm.
+//   Wave mode (P.upd_shared == 0): each wavefront takes one cluster.
+//   Shared mode: the workgroup takes one cluster (problems whose clusters average many
+//   members). The member list goes 256 at a time: each wavefront loads the rows of its 64
+//   consecutive members at once, then the wavefronts add their rows in turn, the running sum
+//   passing through LDS, so the result is still the token-order fp32 sum while the row
+//   loads of the whole 256-member stretch overlap.
+constexpr int kUpdateWaves = 4;
+
+__device__ __forceinline__ int km_update_problem(const KmArgs& a, int block) {
+    int p = 0;
+    while (p + 1 < a.num && !(block >= a.p[p].upd_begin && block < a.p[p].upd_begin + a.p[p].upd_blocks)) ++p;
+    return p;
+}
+
 template <int DT, int D>
-__global__ __launch_bounds__(64) void km_update_kernel(KmArgs a, KmIter it) {
+__global__ __launch_bounds__(kUpdateWaves * kWave) void km_update_kernel(KmArgs a, KmIter it) {
     constexpr int PER = D / kWave;  // channels per lane (1 or 2)
-    __shared__ float row[D];
-    const int p = km_problem(a, blockIdx.x, false);
+    __shared__ float row[kUpdateWaves][D];
+    __shared__ float carry[D];
+    const int p = km_update_problem(a, blockIdx.x);
     const KmProblem& P = a.p[p];
-    const int local = blockIdx.x - P.update_begin;  // b * K + j
     const int K = P.clusters;
-    const int b = local / K;
-    const int j = local % K;
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int local = blockIdx.x - P.upd_begin;
+    const bool shared = P.upd_shared != 0;
+    const int cl = shared ? local : local * kUpdateWaves + wave;  // b * K + j
+    if (cl >= P.batch * K) return;  // wave mode only: the last workgroup may be partial
+    const int b = cl / K;
+    const int j = cl % K;
     const int32_t* off = P.offsets + static_cast<int64_t>(b) * (K + 1);
     const int begin = off[j], end = off[j + 1];
     const int32_t* idx = P.indices + static_cast<int64_t>(b) * P.tokens;
-    const int64_t xbase = static_cast<int64_t>(b) * P.x_stride + lane * PER;
+    const XRows xr = x_rows<DT, D>(P.x, static_cast<int64_t>(b) * P.x_stride, P.tokens, lane);
     float s[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) s[i] = 0.0f;
-    // Member indices arrive 64 at a time (one per lane) and are broadcast with readlane.
-    for (int m0 = begin; m0 < end; m0 += kWave) {
-        const int cnt = min(kWave, end - m0);
-        const int mine = idx[m0 + (lane < cnt ? lane : 0)];
-        add_members<DT, PER>(P.x, xbase, mine, cnt, s);
+    if (!shared) {
+        // Member indices arrive 64 at a time (one per lane) and are broadcast with readlane.
+        for (int m0 = begin; m0 < end; m0 += kWave) {
+            const int cnt = min(kWave, end - m0);
+            const int mine = idx[m0 + (lane < cnt ? lane : 0)];
+            add_members<DT, PER>(xr, mine, cnt, s);
+        }
+    } else {
+        for (int base = begin; base < end; base += kUpdateWaves * kWave) {
+            const int seg = base + kWave * wave;
+            const int cnt = min(kWave, end - seg);  // <= 0: no members in this stretch
+            MemberRows<DT, PER, kWave> rows;
+            if (cnt > 0) {
+                const int mine = idx[seg + min(lane, cnt - 1)];
+                load_member_rows<DT, PER, kWave>(xr, mine, cnt, rows);
+            }
+            // Turns: wavefront w adds its rows between the workgroup's barriers w and w + 1
+            // (every wavefront passes kUpdateWaves barriers per stretch).
+            for (int w = 0; w < wave; ++w) __syncthreads();
+            if (cnt > 0) {
+                if (wave > 0 || base > begin) {
+#pragma unroll
+                    for (int i = 0; i < PER; ++i) s[i] = carry[lane * PER + i];
+                }
+                fold_member_rows<DT, PER, kWave>(rows, cnt, s);
+#pragma unroll
+                for (int i = 0; i < PER; ++i) carry[lane * PER + i] = s[i];
+            }
+            for (int w = wave; w < kUpdateWaves; ++w) __syncthreads();
+        }
+        if (wave != 0) return;
+        if (end > begin) {
+#pragma unroll
+            for (int i = 0; i < PER; ++i) s[i] = carry[lane * PER + i];
+        }
     }
     const int count = end - begin;
-    const int64_t cbase = static_cast<int64_t>(local) * D + lane * PER;
+    const int64_t cbase = static_cast<int64_t>(cl) * D + lane * PER;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const float mean = count > 0 ? s[i] / static_cast<float>(count) : it.src[p][cbase + i];
         it.dst[p][cbase + i] = mean;
         if (P.sums) P.sums[cbase + i] = s[i];
-        row[lane * PER + i] = mean;
+        row[wave][lane * PER + i] = mean;
         uint16_t hi, lo;
         split_neg2(mean, hi, lo);
         P.prep_hi[cbase + i] = hi;
         P.prep_lo[cbase + i] = lo;
     }
-    __syncthreads();
-    if (lane == 0) P.norms[local] = canonical_norm_lds(row, D);
+    // The row is read back by lane 0 of this wavefront only.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane == 0) P.norms[cl] = canonical_norm_lds(row[wave], D);
 }
 
 constexpr int kScanWaves = 8;     // clusters per update workgroup (one per wavefront)
@@ -629,7 +745,7 @@ __global__ __launch_bounds__(kScanWaves * kWave) void km_update_scan_kernel(KmAr
     const int j = (local % groups) * kScanWaves + wave;
     const bool active = j < K;
     const int32_t* labels = P.labels + static_cast<int64_t>(b) * P.tokens;
-    const int64_t xbase = static_cast<int64_t>(b) * P.x_stride + lane * PER;
+    const XRows xr = x_rows<DT, D>(P.x, static_cast<int64_t>(b) * P.x_stride, P.tokens, lane);
     int32_t* q = ring[wave];
     float s[PER];
 #pragma unroll
@@ -642,7 +758,7 @@ __global__ __launch_bounds__(kScanWaves * kWave) void km_update_scan_kernel(KmAr
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         const int mine = q[(head + (lane < cnt ? lane : 0)) & (kRing - 1)];
-        add_members<DT, PER>(P.x, xbase, mine, cnt, s);
+        add_members<DT, PER>(xr, mine, cnt, s);
         __builtin_amdgcn_wave_barrier();  // ring slots are rewritten only after `mine` is read
         head += cnt;
     };
@@ -709,7 +825,8 @@ hipError_t run_fit(KmArgs& a, const KmIter* iters, int iterations, const SortArg
         hipLaunchKernelGGL((km_assign_kernel<DT, D>), dim3(a.total_assign_blocks), dim3(256), 0, s, a, iters[i]);
         hipError_t e = launch_cluster_sort(sa, s, false);
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL((km_update_kernel<DT, D>), dim3(a.total_update_blocks), dim3(64), 0, s, a, iters[i]);
+        hipLaunchKernelGGL((km_update_kernel<DT, D>), dim3(a.total_upd_blocks), dim3(kUpdateWaves * kWave), 0, s, a,
+                           iters[i]);
     }
     return hipGetLastError();
 }
@@ -798,6 +915,10 @@ hipError_t km_fit(const KmFitDesc* descs, int num, int dims, int dtype, int iter
         ab += P.assign_blocks;
         ub += d.batch * d.clusters;
         P.scan_blocks = d.batch * static_cast<int>(ceil_div(d.clusters, kScanWaves));
+        // Clusters averaging more than one row batch (64 members) take a workgroup each.
+        P.upd_shared = d.tokens > 64 * d.clusters ? 1 : 0;
+        P.upd_blocks = P.upd_shared ? d.batch * d.clusters
+                                    : static_cast<int>(ceil_div(static_cast<int64_t>(d.batch) * d.clusters, kUpdateWaves));
         SortProblem& q = sa.p[i];
         q.labels = d.labels;
         q.indices = d.indices;
@@ -816,14 +937,17 @@ hipError_t km_fit(const KmFitDesc* descs, int num, int dims, int dtype, int iter
     {
         int order[kMaxKm] = {0, 1};
         if (num == 2 && a.p[1].clusters > a.p[0].clusters) std::swap(order[0], order[1]);
-        int begin = 0, scan = 0;
+        int begin = 0, scan = 0, upd = 0;
         for (int i = 0; i < num; ++i) {
             a.p[order[i]].assign_begin = begin;
             begin += a.p[order[i]].assign_blocks;
             a.p[order[num - 1 - i]].scan_begin = scan;
             scan += a.p[order[num - 1 - i]].scan_blocks;
+            a.p[order[num - 1 - i]].upd_begin = upd;
+            upd += a.p[order[num - 1 - i]].upd_blocks;
         }
         a.total_scan_blocks = scan;
+        a.total_upd_blocks = upd;
     }
     a.kappa = km_kappa(dtype, dims);
     a.gamma_acc = static_cast<float>(gamma_n(3.0 * dims + 2));
