@@ -207,6 +207,8 @@ __device__ __forceinline__ void split_x8(const XChunk<DT>& r, bool valid, u16x8&
 constexpr float kFarAway = 1.0e37f;
 // Screened values kept per token and lane half (candidates for the canonical recheck).
 constexpr int kTop = 3;
+// VALU instructions of the candidate tracking placed after each screen MFMA.
+constexpr int kTrackValuPerMfma = 5;
 
 template <int D> struct AssignTiles {
     static constexpr int kRow = D + 8;                 // padded LDS row (16-bit elements)
@@ -413,13 +415,27 @@ __global__ __launch_bounds__(256, 2) void km_assign_kernel(KmArgs a, KmIter it) 
     // Software pipeline over centre blocks: the MFMAs of block blk+1 are issued before the
     // VALU tracking of block blk, so the two overlap. Block b sits in LDS buffer b & 1; block
     // blk+2 is fetched into registers and stored into the buffer block blk has left.
+    // Only called while a next block exists, so the screen and the tracking form one basic
+    // block whose MFMAs and VALU instructions are interleaved explicitly (one MFMA, then a
+    // share of the tracking) and execute overlapped within the wavefront.
     auto step = [&](int blk, const f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
-        const bool has1 = blk + 1 < nblocks, has2 = blk + 2 < nblocks;
+        const bool has2 = blk + 2 < nblocks;
         if (has2) load_centres<D>(regs, hi_base, lo_base, norms, (blk + 2) * 32, K, tid);
-        if (has1) screen((blk + 1) & 1, nxt);
+        screen((blk + 1) & 1, nxt);
         track(blk, cur);
+        constexpr int kMfma = S * 2 * (kSplitX ? 3 : 2);
+#pragma unroll
+        for (int i = 0; i < kMfma; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, kTrackValuPerMfma, 0);
+        }
+        // Uses of the candidate lists keep the tracking in this block (it would otherwise
+        // be sunk past the barrier into the next block's tracking).
+#pragma unroll
+        for (int c = 0; c < 2; ++c) asm volatile("" ::"v"(t[c][0]), "v"(t[c][1]), "v"(t[c][2]));
+        __builtin_amdgcn_sched_barrier(0);
         if (has2) store_centres<D>(regs, chi[blk & 1], clo[blk & 1], cn[blk & 1], tid);
-        if (has1) __syncthreads();
+        __syncthreads();
     };
     // With split x (fp16/fp32 input) at D = 128 the second accumulator set does not fit in
     // registers; those fits keep one set and screen, then track, each block in turn.
@@ -433,9 +449,16 @@ __global__ __launch_bounds__(256, 2) void km_assign_kernel(KmArgs a, KmIter it) 
             store_centres<D>(regs, chi[1], clo[1], cn[1], tid);
             __syncthreads();
         }
-        for (int blk = 0; blk < nblocks; blk += 2) {
+        int blk = 0;
+        for (; blk + 2 < nblocks; blk += 2) {
             step(blk, acc_a, acc_b);
-            if (blk + 1 < nblocks) step(blk + 1, acc_b, acc_a);
+            step(blk + 1, acc_b, acc_a);
+        }
+        if (blk + 1 < nblocks) {
+            step(blk, acc_a, acc_b);
+            track(blk + 1, acc_b);
+        } else {
+            track(blk, acc_a);
         }
     } else {
         for (int blk = 0; blk < nblocks; ++blk) {
