@@ -48,6 +48,11 @@ def _oracle_layer(wl, iterations):
     ("hunyuan_480p", 2, 6750),
     ("hunyuan_480p_bo4", 2, 6750),
     ("cpu_small", 2, 2048),
+    # The 720p and 544p Zipf configurations at one head and a shortened sequence: their
+    # cluster counts (256/1024 and 128/512), iteration counts, keep ratios, Base-Offset and
+    # mixture weights are kept, so small and heavily skewed clusters are exercised.
+    ("hunyuan_720p", 1, 12000),
+    ("hunyuan_544p_zipf", 1, 16384),
 ])
 def test_layer_matches_oracle(announce, name, heads, video):
     wl = workloads.make_workload(name, heads=heads, video=video)
@@ -77,3 +82,43 @@ def test_layer_matches_oracle(announce, name, heads, video):
           f"label agreement {agree:.6f}", flush=True)
     assert err.mean().item() <= 2e-3
     assert err.max().item() <= 2e-2
+
+
+def test_layer_warm_start_second_step(announce):
+    """Two denoising steps of the skewed (Zipf) workload. Both calls find cached centroids
+    (the first the seeded initial ones, the second the first call's result) and so run the
+    warm-start iteration count; the second runs on drifted Q/K. Each step's permutations,
+    centroids and output are checked against the oracle started from the oracle's own
+    previous centroids."""
+    wl = workloads.make_workload("hunyuan_544p_zipf", heads=1, video=8192)
+    shape = wl.shape
+    announce(f"warm start: heads=1 video={shape.video} init={shape.iterations} step={shape.warm_iterations}")
+    cfg = processor.PecoConfig(num_q_centroids=shape.num_q_centroids, num_k_centroids=shape.num_k_centroids,
+                               top_p=wl.top_p, min_kc_ratio=wl.min_kc_ratio, kmeans_iter_init=shape.iterations,
+                               kmeans_iter_step=shape.warm_iterations, warmup_steps=0, base_offset_bits=shape.bits)
+    ctx = processor.InferenceContext(step=0, text_length=shape.text, valid_text_length=shape.text)
+    layer = processor.PecoAttention(0, cfg, ctx)
+    layer.q_centroids, layer.k_centroids = wl.q_init.to(DEV), wl.k_init.to(DEV)
+    n = shape.video
+    q_init, k_init = wl.q_init, wl.k_init
+    for step, iters in ((0, shape.warm_iterations), (1, shape.warm_iterations)):
+        cur = wl if step == 0 else workloads.drift(wl, step)
+        with torch.no_grad():
+            out = layer.attention(cur.query.to(DEV), cur.key.to(DEV), cur.value.to(DEV))
+        torch.cuda.synchronize()
+        ref, _ = _oracle_layer(workloads.Workload(shape, cur.query, cur.key, cur.value, q_init, k_init), iters)
+        xq = cur.query[0, :, :n].float().numpy()
+        xk = cur.key[0, :, :n].float().numpy()
+        _, qc, _, qidx, _ = canonical.kmeans_fit(xq, q_init.numpy(), iters)
+        _, kc, _, kidx, _ = canonical.kmeans_fit(xk, k_init.numpy(), iters)
+        q_idx, k_idx = layer._last_fit
+        assert np.array_equal(q_idx.cpu().numpy(), qidx), f"step {step}: Q permutation"
+        assert np.array_equal(k_idx.cpu().numpy(), kidx), f"step {step}: K permutation"
+        assert np.array_equal(layer.q_centroids.cpu().numpy().view(np.int32), qc.view(np.int32))
+        assert np.array_equal(layer.k_centroids.cpu().numpy().view(np.int32), kc.view(np.int32))
+        err = (out.float().cpu() - ref.float()).abs()
+        print(f"[warm] step {step} ({iters} iterations): max {err.max().item():.3e} "
+              f"mean {err.mean().item():.3e}", flush=True)
+        assert err.mean().item() <= 2e-3
+        assert err.max().item() <= 2e-2
+        q_init, k_init = torch.from_numpy(qc), torch.from_numpy(kc)
