@@ -69,8 +69,12 @@ def run_step(layer, wl, q, k, v, q_init, k_init):
 
 
 def stage_breakdown(layer, wl, q, k, v, q_init, k_init, reps):
-    """Per-stage device time (ms) with events on the current stream, and the realised FLOPs."""
-    from peco_amd import attention_cuda, clustering_cuda, workloads
+    """Per-stage device time (ms) with events on the current stream, and the realised FLOPs.
+
+    The stages follow ``PecoAttention.attention``: with Base-Offset off the attention reads
+    Q/K/V through the sort permutations and the pack stage is empty.
+    """
+    from peco_amd import clustering_cuda, workloads
 
     s = wl.shape
     n, dim, heads = s.video, s.dims, s.heads
@@ -89,34 +93,44 @@ def stage_breakdown(layer, wl, q, k, v, q_init, k_init, reps):
             layer.q_centroids.reshape(1, heads, -1, dim), layer.k_centroids.reshape(1, heads, -1, dim), qs, ks,
             wl.top_p, minimum, text=(s.text, s.text))
         ev[2].record()
-        qp, kp, vp = clustering_cuda.pack_clustered([q, k, v], [q_idx, k_idx, k_idx], [ql, kl, None],
-                                                    [layer.q_centroids, layer.k_centroids, None], [s.bits, s.bits, 0],
-                                                    n)
+        if s.bits == 0:
+            attn_args = (q, k, v, emap, eqs, eks, q_idx, k_idx, n)
+        else:
+            qp, kp, vp = clustering_cuda.pack_clustered([q, k, v], [q_idx, k_idx, k_idx], [ql, kl, None],
+                                                        [layer.q_centroids, layer.k_centroids, None],
+                                                        [s.bits, s.bits, 0], n)
+            attn_args = (qp, kp, vp, emap, eqs, eks, q_idx, None, n)
         ev[3].record()
-        attention_cuda.sparse_attention(qp, kp, vp, emap, eqs, eks, validate_sizes=False, out_index=q_idx,
-                                        out_index_rows=n)
+        run_attention(attn_args)
         ev[4].record()
         torch.cuda.synchronize()
         for i, nm in enumerate(names):
             acc[nm] += ev[i].elapsed_time(ev[i + 1])
         flops = workloads.attention_flops(emap, eqs, eks, dim)
-    return {k_: v_ / reps for k_, v_ in acc.items()}, flops, (qp, kp, vp, emap, eqs, eks, q_idx, n)
+    return {k_: v_ / reps for k_, v_ in acc.items()}, flops, attn_args
+
+
+def run_attention(args_):
+    """The layer's attention launch: indexed inputs when k_index is given, else packed ones."""
+    from peco_amd import attention_cuda
+
+    q, k, v, emap, eqs, eks, q_idx, k_idx, rows = args_
+    if k_idx is None:
+        return attention_cuda.sparse_attention(q, k, v, emap, eqs, eks, validate_sizes=False, out_index=q_idx,
+                                               out_index_rows=rows)
+    return attention_cuda.sparse_attention_indexed(q, k, v, emap, eqs, eks, q_idx, k_idx, rows,
+                                                   validate_sizes=False)
 
 
 def attention_kernel_time(args_, reps=20):
     """Average duration of the sparse-attention launch (builder + kernel) on its stream."""
-    from peco_amd import attention_cuda
-
-    qp, kp, vp, emap, eqs, eks, idx, rows = args_
     for _ in range(3):
-        attention_cuda.sparse_attention(qp, kp, vp, emap, eqs, eks, validate_sizes=False, out_index=idx,
-                                        out_index_rows=rows)
+        run_attention(args_)
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(reps):
-        attention_cuda.sparse_attention(qp, kp, vp, emap, eqs, eks, validate_sizes=False, out_index=idx,
-                                        out_index_rows=rows)
+        run_attention(args_)
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / reps
@@ -248,7 +262,8 @@ def main():
                    "kmeans_iterations": s.iterations, "keep_ratio": s.keep_ratio, "base_offset_bits": s.bits},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic(s.name),
-                     "kernel": "sparse_attention (work list + MFMA kernel)", "kernel_ms": round(t_attn, 4),
+                     "kernel": ("sparse_attention_indexed" if attn_args[7] is not None else "sparse_attention")
+                     + " (work list + MFMA kernel)", "kernel_ms": round(t_attn, 4),
                      "flops": flops},
         "stages_ms": {k_: round(v_, 4) for k_, v_ in stages.items()},
         "layer_frac_of_peak": round(value / PEAK_BF16_TFLOPS, 4),

@@ -112,6 +112,16 @@ int peco_sparse_attention_ex(const void* q, const void* k, const void* v, const 
                              int out_index_rows, int* workspace, size_t workspace_ints, int bh, int sq, int sk, int d,
                              int cq, int ck, int dtype, void* stream);
 
+/* peco_sparse_attention_ex on Q/K/V in their original token order: stream row j <
+ * index_rows of head b reads query row q_index[b,j] and key/value row k_index[b,j], and output
+ * row j is written to row q_index[b,j]; later rows (text) keep their position. Fuses the
+ * gather of peco/clustering.py:112-125 (processor.py:143-149) and the restore of
+ * clustering.py:128-136 (processor.py:153-156) into the attention launch. index_rows <= min(sq, sk). */
+int peco_sparse_attention_indexed(const void* q, const void* k, const void* v, const uint8_t* selected,
+                                  const int* q_sizes, const int* k_sizes, void* output, const int32_t* q_index,
+                                  const int32_t* k_index, int index_rows, int* workspace, size_t workspace_ints,
+                                  int bh, int sq, int sk, int d, int cq, int ck, int dtype, void* stream);
+
 /* Cluster-pair selection (replaces the torch ops of peco/clustering.py:140-186), one
  * wavefront per query-cluster row: count-weighted softmax of centroid scores, stable
  * descending order, keep while the preceding mass is < p (all when p == 1), at least

@@ -55,6 +55,58 @@ def _validate(q, k, v, dynamic_map, q_sizes, k_sizes):
     return batch, heads, sq, dim, sk, cq, ck, stride
 
 
+def _check_index(index, name, batch, heads, rows):
+    if not isinstance(index, torch.Tensor) or index.dtype != torch.int32 or not index.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous int32 tensor")
+    if index.numel() != batch * heads * rows:
+        raise ValueError(f"{name} must hold B*H*{rows} elements")
+
+
+def _launch(q, k, v, dynamic_map, q_sizes, k_sizes, validate_sizes, out_index, k_index, rows):
+    batch, heads, sq, dim, sk, cq, ck, stride = _validate(q, k, v, dynamic_map, q_sizes, k_sizes)
+    with torch.cuda.device(q.device):
+        if not _device_is_gfx950(q.device):
+            raise RuntimeError("This HIP build requires an MI355X-class gfx950 GPU")
+        if validate_sizes:
+            torch._assert_async((q_sizes >= 0).all(), "q_sizes must be nonnegative")
+            torch._assert_async((k_sizes >= 0).all(), "k_sizes must be nonnegative")
+            torch._assert_async((q_sizes.sum(-1) == sq).all(), "q_sizes must sum to the Q sequence length")
+            torch._assert_async((k_sizes.sum(-1) == sk).all(), "k_sizes must sum to the K sequence length")
+        output = torch.empty_like(q)
+        if sq == 0:
+            return output
+        rows = sq if rows is None else int(rows)
+        if out_index is not None:
+            if not 0 <= rows <= sq:
+                raise ValueError("out_index_rows must be in [0, SQ]")
+            _check_index(out_index, "out_index", batch, heads, rows)
+        if k_index is not None:
+            if rows > sk:
+                raise ValueError("index_rows must be in [0, min(SQ, SK)]")
+            _check_index(k_index, "k_index", batch, heads, rows)
+            if k_index.device != q.device or out_index.device != q.device:
+                raise ValueError("All sparse attention inputs must reside on the same GPU device")
+        # Same footprint as the reference's workspace (peco/attention_cuda.py:112-113,128).
+        workspace = torch.empty(batch * heads * stride, dtype=torch.int32, device=q.device)
+        library = _native.library()
+        stream = _native.current_stream(q.device, q, k, v, dynamic_map, q_sizes, k_sizes, workspace, output,
+                                        out_index, k_index)
+        dtype = 0 if q.dtype == torch.float16 else 1
+        head = (_native.ptr(q), _native.ptr(k), _native.ptr(v), _native.ptr(dynamic_map), _native.ptr(q_sizes),
+                _native.ptr(k_sizes), _native.ptr(output))
+        tail = (batch * heads, sq, sk, dim, cq, ck, dtype, stream)
+        if k_index is None:
+            error = library.peco_sparse_attention_ex(*head, _native.ptr(out_index), rows, _native.ptr(workspace),
+                                                     workspace.numel(), *tail)
+        else:
+            error = library.peco_sparse_attention_indexed(*head, _native.ptr(out_index), _native.ptr(k_index), rows,
+                                                          _native.ptr(workspace), workspace.numel(), *tail)
+        if error:
+            message = library.peco_attention_error_string(error).decode("utf-8", errors="replace")
+            raise RuntimeError(f"PECO HIP sparse attention launch failed: {message} ({error})")
+        return output
+
+
 def sparse_attention(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -77,34 +129,32 @@ def sparse_attention(
     out_index[b, j] instead (rows j >= R keep their position), fusing the inverse token
     permutation into the epilogue. R is ``out_index_rows`` (default SQ).
     """
-    batch, heads, sq, dim, sk, cq, ck, stride = _validate(q, k, v, dynamic_map, q_sizes, k_sizes)
-    with torch.cuda.device(q.device):
-        if not _device_is_gfx950(q.device):
-            raise RuntimeError("This HIP build requires an MI355X-class gfx950 GPU")
-        if validate_sizes:
-            torch._assert_async((q_sizes >= 0).all(), "q_sizes must be nonnegative")
-            torch._assert_async((k_sizes >= 0).all(), "k_sizes must be nonnegative")
-            torch._assert_async((q_sizes.sum(-1) == sq).all(), "q_sizes must sum to the Q sequence length")
-            torch._assert_async((k_sizes.sum(-1) == sk).all(), "k_sizes must sum to the K sequence length")
-        output = torch.empty_like(q)
-        if sq == 0:
-            return output
-        rows = sq if out_index_rows is None else int(out_index_rows)
-        if out_index is not None:
-            if not 0 <= rows <= sq:
-                raise ValueError("out_index_rows must be in [0, SQ]")
-            if out_index.dtype != torch.int32 or out_index.numel() != batch * heads * rows or not out_index.is_contiguous():
-                raise ValueError("out_index must be a contiguous int32 tensor with B*H*out_index_rows elements")
-        # Same footprint as the reference's workspace (peco/attention_cuda.py:112-113,128).
-        workspace = torch.empty(batch * heads * stride, dtype=torch.int32, device=q.device)
-        library = _native.library()
-        stream = _native.current_stream(q.device, q, k, v, dynamic_map, q_sizes, k_sizes, workspace, output, out_index)
-        error = library.peco_sparse_attention_ex(
-            _native.ptr(q), _native.ptr(k), _native.ptr(v), _native.ptr(dynamic_map), _native.ptr(q_sizes),
-            _native.ptr(k_sizes), _native.ptr(output), _native.ptr(out_index), rows, _native.ptr(workspace),
-            workspace.numel(), batch * heads, sq, sk, dim, cq, ck, 0 if q.dtype == torch.float16 else 1, stream,
-        )
-        if error:
-            message = library.peco_attention_error_string(error).decode("utf-8", errors="replace")
-            raise RuntimeError(f"PECO HIP sparse attention launch failed: {message} ({error})")
-        return output
+    return _launch(q, k, v, dynamic_map, q_sizes, k_sizes, validate_sizes, out_index, None, out_index_rows)
+
+
+def sparse_attention_indexed(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    dynamic_map: torch.Tensor,
+    q_sizes: torch.Tensor,
+    k_sizes: torch.Tensor,
+    q_index: torch.Tensor,
+    k_index: torch.Tensor,
+    index_rows: int,
+    *,
+    validate_sizes: bool = True,
+) -> torch.Tensor:
+    """``sparse_attention`` on Q/K/V left in their original token order.
+
+    The cluster order is given by the sort permutations instead of a packed copy: stream
+    row j < R of head b is query row q_index[b, j] and key/value row k_index[b, j]
+    (R = ``index_rows``, the video length); rows j >= R (text) keep their position. Output
+    row j < R is written to row q_index[b, j], so the result is in original order. Equals
+    ``sparse_attention(gather(q, q_index), gather(k, k_index), gather(v, k_index), ...,
+    out_index=q_index, out_index_rows=R)`` bit for bit, without the gather pass
+    (peco/processor.py:143-156 with the reorder of peco/clustering.py:112-136 fused in).
+    """
+    if q_index is None or k_index is None:
+        raise ValueError("q_index and k_index are required")
+    return _launch(q, k, v, dynamic_map, q_sizes, k_sizes, validate_sizes, q_index, k_index, index_rows)

@@ -31,6 +31,7 @@
 namespace peco {
 namespace {
 
+// s_waitcnt immediate (gfx9 encoding): vmcnt(1), expcnt unchanged, lgkmcnt(0).
 constexpr int kQTile = 128;   // query rows per item (4 waves x 32)
 constexpr int kKTile = 64;    // keys per LDS tile
 constexpr int kSortCap = 2048;
@@ -279,6 +280,15 @@ template <int D> struct Tiles {
 };
 
 
+// One 16-byte-per-lane direct load from global memory into the LDS span starting at byte
+// address lds (M0). Written as inline assembly so that the compiler's wait-count pass does not
+// see an LDS write in flight: it cannot tell the buffer being filled from the one being read
+// by the transpose reads and would otherwise wait for the whole prefetch in the middle of
+// every tile. The caller waits for vmcnt(0) before the barrier that publishes the tile.
+__device__ __forceinline__ void dma16(const uint16_t* src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+
 // Issue the direct-to-LDS loads of one K and one V tile (no wait). Rows past the stream end
 // read row 0 of the head: their K scores are masked to -inf and their P is 0.
 template <int D>
@@ -289,28 +299,36 @@ __device__ __forceinline__ void load_tile_lds(uint16_t* ks, uint16_t* vs, const 
     int rows[T::kLoads];
 #pragma unroll
     for (int i = 0; i < T::kLoads; ++i) rows[i] = prow[(i * 4 + wave) * T::kWaveRows + lane / T::CH];
+    // LDS byte address of this wave's first span in the K tile (wave-uniform) and the distance
+    // from a K span to the matching V span.
+    const uint32_t lds_base = __builtin_amdgcn_readfirstlane(
+        static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ks + wave * kWave * 8)));
+    const uint32_t vs_delta = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(
+        reinterpret_cast<uintptr_t>(vs) - reinterpret_cast<uintptr_t>(ks)));
 #pragma unroll
     for (int i = 0; i < T::kLoads; ++i) {
         const int r = (i * 4 + wave) * T::kWaveRows + lane / T::CH;  // tile row written by this lane
         const int p = lane % T::CH;                                      // physical chunk
         const int64_t g = static_cast<int64_t>(rows[i]) * D;
-        uint16_t* kdst = ks + (i * 4 + wave) * kWave * 8;
-        uint16_t* vdst = vs + (i * 4 + wave) * kWave * 8;
-        __builtin_amdgcn_global_load_lds(kh + g + (p ^ T::swz_k(r)) * 8,
-                                         (__attribute__((address_space(3))) void*)kdst, 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(vh + g + (p ^ T::swz_v(r)) * 8,
-                                         (__attribute__((address_space(3))) void*)vdst, 16, 0, 0);
+        const uint32_t kdst = lds_base + static_cast<uint32_t>(((i * 4) * kWave * 8) * 2);
+        const uint32_t vdst = kdst + vs_delta;
+        dma16(kh + g + (p ^ T::swz_k(r)) * 8, kdst);
+        dma16(vh + g + (p ^ T::swz_v(r)) * 8, vdst);
     }
 #endif
 }
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
-template <int DT, int D>
+// kIndexed: the inputs are in their original token order. Query row j < oi_rows of a head is
+// read from row out_index[j] (the same permutation that scatters the output) and key/value
+// stream row p < oi_rows from row k_index[p]; rows past oi_rows (text) keep their position.
+template <int DT, int D, bool kIndexed>
 __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint8_t* __restrict__ selected, const int32_t* __restrict__ ws, uint16_t* __restrict__ out,
-    const int32_t* __restrict__ out_index, int oi_rows, int bhn, int sq, int sk, int cq, int ck, float scale_log2) {
+    const int32_t* __restrict__ out_index, int oi_rows, const int32_t* __restrict__ k_index, int bhn, int sq,
+    int sk, int cq, int ck, float scale_log2) {
     using T = Tiles<D>;
     constexpr int S = D / 16;       // k-steps of S^T over channels
     constexpr int NB = D / 32;      // 32-channel blocks of O^T
@@ -370,21 +388,37 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
         while (cur + 1 < nk && kof[cur + 1] <= r) ++cur;
         return kst[cur] + (r - kof[cur]);
     };
-    if (tid < kKTile) {
-        prow[0][tid] = tid < L ? row_of(tid) : 0;
-        const int r1 = kKTile + tid;
-        prow[1][tid] = r1 < L ? row_of(r1) : 0;
+    // Indexed inputs: lanes 0..15 of every wave own the tile rows 16*wave + lane, so the index
+    // loads are spread over the waves. The indices of tile t+2 are loaded when tile t starts and
+    // written to prow at its end, so their latency hides behind tile t's MFMAs.
+    const int64_t head = static_cast<int64_t>(bh);
+    const int32_t* kidx = kIndexed ? k_index + head * oi_rows : nullptr;
+    const uint32_t sq_last = static_cast<uint32_t>(sq - 1), sk_last = static_cast<uint32_t>(sk - 1);
+    const bool prow_owner = kIndexed ? lane < 16 : tid < kKTile;
+    const int prow_entry = kIndexed ? 16 * wave + lane : tid;
+    auto stream_row = [&](int r) {
+        const int p = r < L ? row_of(r) : 0;
+        // Index values are clamped to the head's rows, so a bad permutation cannot read out of bounds.
+        if constexpr (kIndexed) return p < oi_rows ? static_cast<int>(min(static_cast<uint32_t>(kidx[p]), sk_last)) : p;
+        else return p;
+    };
+    if (prow_owner) {
+        prow[0][prow_entry] = stream_row(prow_entry);
+        prow[1][prow_entry] = stream_row(kKTile + prow_entry);
     }
 
     // Q^T operand: lane holds query row (32*wave + l%32), channels 16s + 8h .. +7.
     const int qrow = wave * 32 + (lane % 32);
     const bool qvalid = qrow < q_rows;
     const bool wave_active = wave * 32 < q_rows;
-    const int64_t head = static_cast<int64_t>(bh);
+    int64_t qsrc = q_start + qrow;
+    if constexpr (kIndexed) {
+        if (qvalid && qsrc < oi_rows) qsrc = min(static_cast<uint32_t>(out_index[head * oi_rows + qsrc]), sq_last);
+    }
     u16x8 qf[S];
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-        qf[s] = qvalid ? *reinterpret_cast<const u16x8*>(q + (head * sq + q_start + qrow) * D + 16 * s + 8 * h)
+        qf[s] = qvalid ? *reinterpret_cast<const u16x8*>(q + (head * sq + qsrc) * D + 16 * s + 8 * h)
                        : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
     }
     f32x16 oacc[NB];
@@ -406,6 +440,10 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     auto step = [&](auto bufc, int tile) {
         constexpr int buf = decltype(bufc)::value;
         const bool more = tile + 1 < ntiles;
+        int ahead = 0;
+        if constexpr (kIndexed) {
+            if (prow_owner && tile + 2 < ntiles) ahead = stream_row((tile + 2) * kKTile + prow_entry);
+        }
         if (more) load_tile_lds<D>(ks[buf ^ 1], vs[buf ^ 1], kh, vh, prow[buf ^ 1], wave, lane);
         if (wave_active) {
             const int base = tile * kKTile;
@@ -495,9 +533,10 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
                 }
             }
         }
-        if (more && tid < kKTile) {
-            const int r = (tile + 2) * kKTile + tid;
-            prow[buf][tid] = r < L ? row_of(r) : 0;
+        if constexpr (kIndexed) {
+            if (prow_owner && tile + 2 < ntiles) prow[buf][prow_entry] = ahead;
+        } else {
+            if (more && tid < kKTile) prow[buf][tid] = stream_row((tile + 2) * kKTile + tid);
         }
         __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of the next tile have landed
         __syncthreads();
@@ -510,7 +549,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     int64_t orow = q_start + qrow;
-    if (out_index && orow < oi_rows) orow = out_index[head * oi_rows + orow];
+    if (out_index && orow < oi_rows) orow = min(static_cast<uint32_t>(out_index[head * oi_rows + orow]), sq_last);
     uint16_t* o = out + (head * sq + orow) * D;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
@@ -542,16 +581,19 @@ PECO_API size_t peco_sparse_attention_workspace_size(int bh, int sq, int sk, int
            static_cast<size_t>(bh) * item_capacity(sq, cq) * 3;
 }
 
-// Extended entry: out_index (nullable, int32 [bh, out_index_rows]) scatters output row
-// j < out_index_rows of head b to row out_index[b, j] (rows past out_index_rows keep their
-// position), fusing the inverse permutation into the epilogue.
-PECO_API int peco_sparse_attention_ex(const void* q, const void* k, const void* v, const uint8_t* selected,
-                                      const int* q_sizes, const int* k_sizes, void* output, const int32_t* out_index,
-                                      int out_index_rows, int* workspace, size_t workspace_ints, int bh, int sq,
-                                      int sk, int d, int cq, int ck, int dtype, void* stream) {
+namespace peco {
+namespace {
+
+// Shared launcher: k_index (nullable) selects the indexed-input kernel (inputs in original
+// token order, read through out_index for Q and k_index for K/V).
+int launch_sparse_attention(const void* q, const void* k, const void* v, const uint8_t* selected,
+                            const int* q_sizes, const int* k_sizes, void* output, const int32_t* out_index,
+                            int out_index_rows, const int32_t* k_index, int* workspace, size_t workspace_ints,
+                            int bh, int sq, int sk, int d, int cq, int ck, int dtype, void* stream) {
     if (!q || !k || !v || !selected || !q_sizes || !k_sizes || !output || !workspace || bh < 1 || bh > 65535 ||
         sq < 0 || sk < 0 || cq < 1 || ck < 1 || (d != 64 && d != 128) || (dtype != kF16 && dtype != kBF16) ||
-        (out_index && (out_index_rows < 0 || out_index_rows > sq)))
+        (out_index && (out_index_rows < 0 || out_index_rows > sq)) ||
+        (k_index && (!out_index || out_index_rows > sk)))
         return kInvalidValue;
     if (sq == 0) return kOk;
     if (workspace_ints < peco_sparse_attention_workspace_size(bh, sq, sk, cq, ck)) return kWorkspaceTooSmall;
@@ -568,18 +610,52 @@ PECO_API int peco_sparse_attention_ex(const void* q, const void* k, const void* 
     const auto* kp = static_cast<const uint16_t*>(k);
     const auto* vp = static_cast<const uint16_t*>(v);
     auto* op = static_cast<uint16_t*>(output);
-#define PECO_ATTN(DT_, D_)                                                                                        \
-    hipLaunchKernelGGL((sparse_attention_kernel<DT_, D_>), grid, dim3(256), lds_attn, s, qp, kp, vp, selected,    \
-                       workspace, op, out_index, out_index_rows, bh, sq, sk, cq, ck, scale_log2)
+#define PECO_ATTN(DT_, D_, IX_)                                                                                    \
+    hipLaunchKernelGGL((sparse_attention_kernel<DT_, D_, IX_>), grid, dim3(256), lds_attn, s, qp, kp, vp, selected, \
+                       workspace, op, out_index, out_index_rows, k_index, bh, sq, sk, cq, ck, scale_log2)
+#define PECO_ATTN_D(DT_, IX_)                                                                                      \
+    do {                                                                                                           \
+        if (d == 128) PECO_ATTN(DT_, 128, IX_);                                                                    \
+        else PECO_ATTN(DT_, 64, IX_);                                                                              \
+    } while (0)
     if (dtype == kBF16) {
-        if (d == 128) PECO_ATTN(kBF16, 128);
-        else PECO_ATTN(kBF16, 64);
+        if (k_index) PECO_ATTN_D(kBF16, true);
+        else PECO_ATTN_D(kBF16, false);
     } else {
-        if (d == 128) PECO_ATTN(kF16, 128);
-        else PECO_ATTN(kF16, 64);
+        if (k_index) PECO_ATTN_D(kF16, true);
+        else PECO_ATTN_D(kF16, false);
     }
+#undef PECO_ATTN_D
 #undef PECO_ATTN
     return hipGetLastError();
+}
+
+}  // namespace
+}  // namespace peco
+
+// Extended entry: out_index (nullable, int32 [bh, out_index_rows]) scatters output row
+// j < out_index_rows of head b to row out_index[b, j] (rows past out_index_rows keep their
+// position), fusing the inverse permutation into the epilogue.
+PECO_API int peco_sparse_attention_ex(const void* q, const void* k, const void* v, const uint8_t* selected,
+                                      const int* q_sizes, const int* k_sizes, void* output, const int32_t* out_index,
+                                      int out_index_rows, int* workspace, size_t workspace_ints, int bh, int sq,
+                                      int sk, int d, int cq, int ck, int dtype, void* stream) {
+    return launch_sparse_attention(q, k, v, selected, q_sizes, k_sizes, output, out_index, out_index_rows, nullptr,
+                                   workspace, workspace_ints, bh, sq, sk, d, cq, ck, dtype, stream);
+}
+
+// Gathering entry: q, k, v (and output) stay in original token order. The first index_rows
+// rows of each head are read in cluster order through q_index (queries, also the output
+// scatter) and k_index (keys and values), so no packed copies are needed.
+PECO_API int peco_sparse_attention_indexed(const void* q, const void* k, const void* v, const uint8_t* selected,
+                                           const int* q_sizes, const int* k_sizes, void* output,
+                                           const int32_t* q_index, const int32_t* k_index, int index_rows,
+                                           int* workspace, size_t workspace_ints, int bh, int sq, int sk, int d,
+                                           int cq, int ck, int dtype, void* stream) {
+    if (index_rows < 0 || (index_rows > 0 && (!q_index || !k_index))) return kInvalidValue;
+    if (index_rows == 0) q_index = k_index = nullptr;  // nothing is permuted
+    return launch_sparse_attention(q, k, v, selected, q_sizes, k_sizes, output, q_index, index_rows, k_index,
+                                   workspace, workspace_ints, bh, sq, sk, d, cq, ck, dtype, stream);
 }
 
 // Reference ABI (peco/kernels/sparse_attention.cu:210): workspace holds

@@ -20,7 +20,7 @@ import torch.nn.functional as F
 from torch.nn.attention import SDPBackend, sdpa_kernel
 
 from . import clustering_cuda
-from .attention_cuda import sparse_attention
+from .attention_cuda import sparse_attention, sparse_attention_indexed
 from .quantization import _validate_bits
 
 
@@ -199,6 +199,11 @@ class PecoAttention:
             self.q_centroids.reshape(batch, heads, -1, dim), self.k_centroids.reshape(batch, heads, -1, dim),
             q_sizes, k_sizes, self.config.top_p,
             math.ceil(self.config.min_kc_ratio * self.config.num_k_centroids), text=(valid_text, text_length))
+        if bits == 0:
+            # No fake quantization: attention reads Q/K/V through the sort permutations and
+            # writes the output in original order, so no packed copy is made.
+            return sparse_attention_indexed(query, key, value, dynamic_map, q_sizes, k_sizes, q_idx, k_idx,
+                                            video_length, validate_sizes=False)
         # Fake-quantize Q/K against their centroids while packing Q/K/V into cluster order.
         q_perm, k_perm, v_perm = clustering_cuda.pack_clustered(
             [query, key, value], [q_idx, k_idx, k_idx], [q_labels, k_labels, None],

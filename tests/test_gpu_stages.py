@@ -314,6 +314,46 @@ def test_sparse_attention_out_index_scatter(announce):
     assert torch.equal(fused.cpu().view(torch.int16), restored.cpu().view(torch.int16))
 
 
+def _gather_rows(x, index):
+    """x [1,H,S,D] with rows j < R of head h replaced by rows index[h, j]."""
+    out = x.clone()
+    rows = index.shape[1]
+    out[0, :, :rows] = x[0].gather(1, index.long()[..., None].expand(-1, -1, x.shape[-1]))
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dims", [128, 64])
+@pytest.mark.parametrize("sq,sk,rows", [(1000, 1000, 900), (700, 1100, 650), (300, 300, 300), (260, 260, 0)])
+def test_sparse_attention_indexed_equals_packed(announce, dtype, dims, sq, sk, rows):
+    """Reading Q/K/V through the sort permutations gives the packed path's output bit for bit."""
+    g = _gen(sq + rows + dims)
+    h, cq, ck = 3, 7, 11
+    q = torch.randn(1, h, sq, dims, generator=g).to(dtype)
+    k = torch.randn(1, h, sk, dims, generator=g).to(dtype)
+    v = torch.randn(1, h, sk, dims, generator=g).to(dtype)
+    qs = torch.stack([_random_partition(g, sq, cq, empty=1) for _ in range(h)])[None]
+    ks = torch.stack([_random_partition(g, sk, ck, empty=2) for _ in range(h)])[None]
+    m = torch.rand(1, h, cq, ck, generator=g) < 0.4
+    m[0, 1, 3] = False  # a fully masked query cluster
+    qi = torch.stack([torch.randperm(rows, generator=g) for _ in range(h)]).to(torch.int32)
+    ki = torch.stack([torch.randperm(rows, generator=g) for _ in range(h)]).to(torch.int32)
+    announce(f"{dtype} D={dims} sq={sq} sk={sk} rows={rows}")
+    dev = [t.to(DEV) for t in (q, k, v, m, qs, ks, qi, ki)]
+    indexed = attention_cuda.sparse_attention_indexed(*dev[:6], dev[6], dev[7], rows)
+    packed = attention_cuda.sparse_attention(_gather_rows(dev[0], dev[6]), _gather_rows(dev[1], dev[7]),
+                                             _gather_rows(dev[2], dev[7]), *dev[3:6], out_index=dev[6],
+                                             out_index_rows=rows)
+    assert torch.equal(indexed.cpu().view(torch.int16), packed.cpu().view(torch.int16))
+    # And against the oracle on the packed inputs, restored to original order.
+    pq, pk, pv = (_gather_rows(x, i)[0].float().numpy() for x, i in ((q, qi), (k, ki), (v, ki)))
+    ref = canonical.sparse_attention(pq, pk, pv, m[0].numpy(), qs[0].numpy(), ks[0].numpy())
+    restored = np.array(ref)
+    for head in range(h):
+        restored[head, qi[head].long().numpy()] = ref[head, :rows]
+    _check_attention(indexed[0], restored)
+
+
 # ---------------------------------------------------------------- selection + text partition
 
 @pytest.mark.parametrize("p,ratio", [(1e-9, 0.25), (0.5, 0.0), (0.9, 0.1), (1.0, 0.0), (0.0, 0.0)])
