@@ -46,6 +46,9 @@ def parse():
                          "(for rocprofv3 counter runs)")
     ap.add_argument("--reps", type=int, default=10)
     ap.add_argument("--copy-mib", type=int, default=1024)
+    ap.add_argument("--sequence", action="store_true",
+                    help="time the workload's denoising sequence: its `steps` layer calls on drifting Q/K, the "
+                         "first from the seeded centroids, the rest warm-started from the previous call's centroids")
     ap.add_argument("--summarize", metavar="CSV", default=None,
                     help="print per-kernel averages of a rocprofv3 counter_collection.csv or kernel_stats.csv")
     return ap.parse_args()
@@ -220,6 +223,91 @@ def profile_target(args):
           flush=True)
 
 
+def run_sequence(args):
+    """Multi-step scenario: one repetition = the workload's `steps` calls of one layer on Q/K
+    drifting by N(0, drift^2) per step (V fixed), k-means warm-started between calls.
+
+    Call 0 fits from the seeded centroids with `iterations` Lloyd iterations; calls 1.. start
+    from the layer's cached centroids with `warm_iterations` (PecoAttention's kmeans_iter_step),
+    as PecoAttention.attention does across denoising steps (peco/processor.py:98-113). All
+    inputs are generated before timing. value = sum of the calls' F4 / sequence time.
+    """
+    from peco_amd import clustering_cuda, processor, workloads
+
+    dev = torch.device("cuda:0")
+    wl = workloads.make_workload(args.workload, device=dev)
+    s = wl.shape
+    calls = max(1, s.steps)
+    inputs = [wl]
+    for step in range(1, calls):
+        inputs.append(workloads.drift(inputs[-1], step))
+    layer = make_layer(wl)
+    first_cfg = layer.config
+    warm_cfg = processor.PecoConfig(**{**first_cfg.__dict__, "kmeans_iter_step": s.warm_iterations or s.iterations})
+
+    def sequence(times=None):
+        outs = []
+        for i, cur in enumerate(inputs):
+            if times is not None:
+                ev = torch.cuda.Event(enable_timing=True)
+                ev.record()
+                times.append(ev)
+            if i == 0:
+                layer.config = first_cfg
+                layer.q_centroids, layer.k_centroids = wl.q_init, wl.k_init
+            else:
+                layer.config = warm_cfg
+            outs.append(layer.attention(cur.query, cur.key, cur.value))
+        if times is not None:
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record()
+            times.append(ev)
+        return outs
+
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            sequence()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            sequence()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / args.steps
+        evs = []
+        sequence(evs)
+        torch.cuda.synchronize()
+        call_ms = [evs[i].elapsed_time(evs[i + 1]) for i in range(calls)]
+        # Realised F4 of every call: the same fits (bit-exact) rerun with the selection.
+        flops = []
+        n, dim = s.video, s.dims
+        minimum = math.ceil(wl.min_kc_ratio * s.num_k_centroids)
+        for i, cur in enumerate(inputs):
+            layer.config = first_cfg if i == 0 else warm_cfg
+            if i == 0:
+                layer.q_centroids, layer.k_centroids = wl.q_init, wl.k_init
+            _, _, qs, ks = layer._update_cluster_state(cur.query[:, :, :n], cur.key[:, :, :n])
+            emap, eqs, eks = clustering_cuda.select_connections(
+                layer.q_centroids.reshape(1, s.heads, -1, dim), layer.k_centroids.reshape(1, s.heads, -1, dim), qs,
+                ks, wl.top_p, minimum, text=(s.text, s.text))
+            flops.append(workloads.attention_flops(emap, eqs, eks, dim))
+    total = sum(flops)
+    value = total / (ms * 1e-3) / 1e12
+    line = {
+        "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": s.name, "heads": s.heads, "video_tokens": s.video, "text_tokens": s.text,
+                   "head_dim": s.dims, "q_clusters": s.num_q_centroids, "k_clusters": s.num_k_centroids,
+                   "kmeans_iterations": s.iterations, "warm_iterations": s.warm_iterations, "drift": s.drift,
+                   "keep_ratio": s.keep_ratio, "base_offset_bits": s.bits, "layer_calls_per_step": calls},
+        "sequence": {"call_ms": [round(t, 4) for t in call_ms], "call_flops": flops,
+                     "first_call_ms": round(call_ms[0], 4),
+                     "warm_call_ms": round(sum(call_ms[1:]) / max(1, calls - 1), 4)},
+        "layer_frac_of_peak": round(value / PEAK_BF16_TFLOPS, 4),
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     if args.summarize:
@@ -232,6 +320,9 @@ def main():
         print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are not part of it",
                           "n_gpus": args.gpus}))
         sys.exit(2)
+    if args.sequence:
+        run_sequence(args)
+        return
     from peco_amd import workloads
 
     dev = torch.device("cuda:0")

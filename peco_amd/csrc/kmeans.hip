@@ -47,7 +47,8 @@ struct KmProblem {
     uint16_t* prep_hi;      // [batch, K, D] bf16(-2 c)
     uint16_t* prep_lo;      // [batch, K, D] bf16(-2 c - hi)
     float* norms;           // [batch, K] canonical norms of the current centres
-    int32_t* tile_hist;     // [batch, sort tiles, K]
+    int32_t* tile_hist;     // [batch, sort tiles, K] (cleared by the prep kernel)
+    int32_t* tile_hist2;    // nullable second histogram set: alternates with tile_hist per iteration
     float* sums;            // nullable [batch, K, D]: per-cluster sums of the last update
     int batch, tokens, clusters;
     int assign_begin;       // first linear assign block of this problem
@@ -78,7 +79,7 @@ struct KmArgs {
 struct KmIter {
     const float* src[kMaxKm];  // centres used by this iteration
     float* dst[kMaxKm];        // means written by this iteration
-    int hist;                  // assign adds its labels to the sort tile histograms
+    int32_t* hist[kMaxKm];     // nullable: tile histograms the assign adds its labels to
 };
 
 namespace {
@@ -538,8 +539,8 @@ __global__ __launch_bounds__(256, 2) void km_assign_kernel(KmArgs a, KmIter it) 
         }
         if (valid[c] && h == 0) {
             P.labels[static_cast<int64_t>(b) * P.tokens + tok[c]] = label;
-            if (it.hist)
-                atomicAdd(P.tile_hist + (static_cast<int64_t>(b) * P.sort_tiles + tok[c] / kSortTile) * K + label, 1);
+            if (it.hist[p])
+                atomicAdd(it.hist[p] + (static_cast<int64_t>(b) * P.sort_tiles + tok[c] / kSortTile) * K + label, 1);
         }
     }
 }
@@ -842,10 +843,16 @@ __global__ __launch_bounds__(kScanWaves * kWave) void km_update_scan_kernel(KmAr
 }
 
 template <int DT, int D>
-hipError_t run_fit(KmArgs& a, const KmIter* iters, int iterations, const SortArgs& sa, hipStream_t s) {
+hipError_t run_fit(KmArgs& a, const KmIter* iters, int iterations, SortArgs sa, hipStream_t s) {
     hipLaunchKernelGGL((km_prep_kernel<D>), dim3(a.total_update_blocks), dim3(64), 0, s, a, iters[0]);
     for (int i = 0; i < iterations; ++i) {
         hipLaunchKernelGGL((km_assign_kernel<DT, D>), dim3(a.total_assign_blocks), dim3(256), 0, s, a, iters[i]);
+        // The sort reads the histograms this iteration's assign filled. The fused sort leaves
+        // them intact and clears the other set, which the next iteration's assign fills.
+        for (int q = 0; q < a.num; ++q) {
+            sa.p[q].tile_hist = iters[i].hist[q];
+            sa.p[q].next_hist = sa.fused ? (i % 2 == 0 ? a.p[q].tile_hist2 : a.p[q].tile_hist) : nullptr;
+        }
         hipError_t e = launch_cluster_sort(sa, s, false);
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL((km_update_kernel<DT, D>), dim3(a.total_upd_blocks), dim3(kUpdateWaves * kWave), 0, s, a,
@@ -894,6 +901,7 @@ size_t km_workspace_bytes(int batch, int tokens, int clusters, int dims) {
     add(bkd * sizeof(uint16_t));                    // prep lo
     add(static_cast<size_t>(batch) * clusters * sizeof(float));  // norms
     add(sort_workspace_ints(batch, tokens, clusters) * sizeof(int32_t));
+    if (sort_fusable(tokens, clusters)) add(sort_workspace_ints(batch, tokens, clusters) * sizeof(int32_t));
     return bytes;
 }
 
@@ -924,6 +932,10 @@ hipError_t km_fit(const KmFitDesc* descs, int num, int dims, int dtype, int iter
         P.prep_lo = reinterpret_cast<uint16_t*>(take(bkd * sizeof(uint16_t)));
         P.norms = reinterpret_cast<float*>(take(static_cast<size_t>(d.batch) * d.clusters * sizeof(float)));
         P.tile_hist = reinterpret_cast<int32_t*>(take(sort_workspace_ints(d.batch, d.tokens, d.clusters) * sizeof(int32_t)));
+        P.tile_hist2 = sort_fusable(d.tokens, d.clusters)
+                           ? reinterpret_cast<int32_t*>(take(sort_workspace_ints(d.batch, d.tokens, d.clusters) *
+                                                             sizeof(int32_t)))
+                           : nullptr;
         P.labels = d.labels;
         P.counts = d.counts;
         P.indices = d.indices;
@@ -975,6 +987,11 @@ hipError_t km_fit(const KmFitDesc* descs, int num, int dims, int dtype, int iter
     a.kappa = km_kappa(dtype, dims);
     a.gamma_acc = static_cast<float>(gamma_n(3.0 * dims + 2));
     sort_args_finalize(sa);
+    // Small problems (every problem fusable) sort with one fused launch per iteration, which
+    // needs the two alternating histogram sets.
+    sa.fused = 1;
+    for (int i = 0; i < num; ++i)
+        if (!a.p[i].tile_hist2) sa.fused = 0;
     std::vector<KmIter> iters(std::max(iterations, 1));
     for (int i = 0; i < iterations; ++i) {
         for (int q = 0; q < num; ++q) {
@@ -982,7 +999,8 @@ hipError_t km_fit(const KmFitDesc* descs, int num, int dims, int dtype, int iter
             iters[i].dst[q] = dst;
             iters[i].src[q] = i == 0 ? a.p[q].centers_in : iters[i - 1].dst[q];
         }
-        iters[i].hist = 1;
+        for (int q = 0; q < num; ++q)
+            iters[i].hist[q] = (sa.fused && i % 2 == 1) ? a.p[q].tile_hist2 : a.p[q].tile_hist;
     }
 #define PECO_FIT(DT_, D_) return run_fit<DT_, D_>(a, iters.data(), iterations, sa, stream)
     if (dims == 128) {

@@ -221,6 +221,128 @@ __global__ __launch_bounds__(64) void sort_place_kernel(SortArgs args) {
     }
 }
 
+__device__ __forceinline__ int find_problem_by_group(const SortArgs& a, int group) {
+    int p = 0;
+    while (p + 1 < a.num && group >= a.p[p + 1].group_begin) ++p;
+    return p;
+}
+
+// Scan and place in one launch for small batch entries (sort_fusable). Workgroup (b, g)
+// ranks tiles kFusedTiles*g .. +3, one per wavefront. Every workgroup of entry b loads the
+// whole tile histogram of b (at most kFusedMaxTiles rows, all in flight per cluster) and
+// computes the cluster totals, their exclusive scan and its own tiles' run starts, so the
+// result equals sort_scan followed by sort_place. The histogram is left unchanged (other
+// workgroups still read it); next_hist, when given, is cleared for the next producer.
+__global__ __launch_bounds__(256) void sort_fused_kernel(SortArgs args) {
+    extern __shared__ int lds[];  // [kFusedTiles][K] run starts, then [K] cluster offsets
+    __shared__ int tmp[4];
+    const int pi = find_problem_by_group(args, blockIdx.x);
+    const SortProblem& P = args.p[pi];
+    const int groups = static_cast<int>(ceil_div(P.tiles, kFusedTiles));
+    const int local = blockIdx.x - P.group_begin;
+    const int b = local / groups;
+    const int g = local % groups;
+    const int K = P.clusters;
+    const int tiles = P.tiles;
+    const int wave = threadIdx.x / kWave;
+    const int lane = lane_id();
+    const int tile = g * kFusedTiles + wave;
+    const int begin = tile * kSortTile;
+    const int end = min(P.tokens, begin + kSortTile);
+    const int32_t* lab = P.labels + static_cast<int64_t>(b) * P.tokens;
+    // This wavefront's labels first, so their loads overlap the histogram loads below.
+    constexpr int kSteps = kSortTile / kWave;
+    int labs[kSteps];
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st) {
+        const int t = begin + st * kWave + lane;
+        const int raw = lab[min(t, P.tokens - 1)];  // clamped, unconditional: all loads in flight
+        labs[st] = t < end ? raw : -1;
+    }
+    int* starts = lds;
+    int* offs = lds + kFusedTiles * K;
+    const int32_t* th = P.tile_hist + static_cast<int64_t>(b) * tiles * K;
+    const int first = g * kFusedTiles;
+    for (int k = threadIdx.x; k < K; k += blockDim.x) {
+        int c[kFusedMaxTiles];
+#pragma unroll
+        for (int t = 0; t < kFusedMaxTiles; ++t) {
+            const int v = th[static_cast<int64_t>(min(t, tiles - 1)) * K + k];
+            c[t] = t < tiles ? v : 0;
+        }
+        int run = 0;  // tokens of cluster k in tiles before t
+#pragma unroll
+        for (int t = 0; t < kFusedMaxTiles; ++t) {
+            const int w = t - first;
+            if (w >= 0 && w < kFusedTiles) starts[w * K + k] = run;
+            run += c[t];
+        }
+        offs[k] = run;  // the cluster's total for now
+    }
+    __syncthreads();
+    // Exclusive scan of the totals over clusters (each thread owns a contiguous chunk).
+    const int per = static_cast<int>(ceil_div(K, blockDim.x));
+    const int k0 = min(K, static_cast<int>(threadIdx.x) * per);
+    const int k1 = min(K, k0 + per);
+    int chunk = 0;
+    for (int k = k0; k < k1; ++k) chunk += offs[k];
+    int total = 0;
+    int run = block_exclusive_scan256(chunk, tmp, &total);
+    int32_t* off = P.offsets + static_cast<int64_t>(b) * (K + 1);
+    int32_t* counts = P.counts ? P.counts + static_cast<int64_t>(b) * K : nullptr;
+    for (int k = k0; k < k1; ++k) {
+        const int c = offs[k];
+        if (g == 0) {
+            off[k] = run;
+            if (counts) counts[k] = c;
+        }
+        offs[k] = run;
+        run += c;
+    }
+    if (g == 0 && threadIdx.x == 0) off[K] = total;
+    __syncthreads();
+    if (P.next_hist) {
+        // Clear this workgroup's tiles in the histogram the next producer accumulates into.
+        const int rows = min(kFusedTiles, tiles - first);
+        int32_t* nh = P.next_hist + (static_cast<int64_t>(b) * tiles + first) * K;
+        for (int i = threadIdx.x; i < rows * K; i += blockDim.x) nh[i] = 0;
+    }
+    if (tile >= tiles) return;
+    // Rank this wavefront's tile as sort_place does, from its own run starts.
+    int* base = starts + wave * K;
+    for (int k = lane; k < K; k += kWave) base[k] += offs[k];
+    __builtin_amdgcn_wave_barrier();
+    const int bits = K > 1 ? 32 - __builtin_clz(static_cast<unsigned>(K - 1)) : 0;
+    int32_t* idx = P.indices + static_cast<int64_t>(b) * P.tokens;
+    int32_t* ranks = P.ranks ? P.ranks + static_cast<int64_t>(b) * P.tokens : nullptr;
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st) {
+        const int t = begin + st * kWave + lane;
+        const int raw = labs[st];
+        const bool active = t < end && static_cast<unsigned>(raw) < static_cast<unsigned>(K);
+        const int L = active ? raw : 0;
+        uint64_t eq = __ballot(active);
+        for (int bit = 0; bit < bits; ++bit) {
+            const bool on = active && ((L >> bit) & 1);
+            const uint64_t m = __ballot(on);
+            eq &= ((L >> bit) & 1) ? m : ~m;
+        }
+        const int rank = __popcll(eq & below);
+        const int cnt = __popcll(eq);
+        const bool last = active && ((eq >> lane) == 1ull);
+        int pos = 0;
+        if (active) pos = base[L] + rank;
+        __builtin_amdgcn_wave_barrier();
+        if (last) base[L] += cnt;
+        __builtin_amdgcn_wave_barrier();
+        if (active) {
+            idx[pos] = t;
+            if (ranks) ranks[t] = pos;
+        }
+    }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void reorder_rows_kernel(const T* __restrict__ in, const int32_t* __restrict__ idx,
                                                            T* __restrict__ out, int tokens, int chunks,
@@ -241,22 +363,32 @@ __global__ __launch_bounds__(256) void reorder_rows_kernel(const T* __restrict__
 }  // namespace
 
 void sort_args_finalize(SortArgs& a) {
-    int blocks = 0, batches = 0;
+    int blocks = 0, batches = 0, groups = 0;
     for (int i = 0; i < a.num; ++i) {
         a.p[i].tiles = sort_tiles(a.p[i].tokens);
         a.p[i].block_begin = blocks;
         a.p[i].batch_begin = batches;
+        a.p[i].group_begin = groups;
         blocks += a.p[i].batch * a.p[i].tiles;
         batches += a.p[i].batch;
+        groups += a.p[i].batch * static_cast<int>(ceil_div(a.p[i].tiles, kFusedTiles));
     }
     a.total_blocks = blocks;
     a.total_batches = batches;
+    a.total_groups = groups;
 }
 
 hipError_t launch_cluster_sort(const SortArgs& args, hipStream_t stream, bool with_hist) {
     int kmax = 1;
     for (int i = 0; i < args.num; ++i) kmax = max(kmax, args.p[i].clusters);
     const size_t lds = sizeof(int) * static_cast<size_t>(kmax);
+    if (args.fused && !with_hist) {
+        for (int i = 0; i < args.num; ++i)
+            if (!sort_fusable(args.p[i].tokens, args.p[i].clusters)) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(sort_fused_kernel, dim3(args.total_groups), dim3(256), (kFusedTiles + 1) * lds, stream,
+                           args);
+        return hipGetLastError();
+    }
     if (with_hist) hipLaunchKernelGGL(sort_hist_kernel, dim3(args.total_blocks), dim3(256), lds, stream, args);
     hipLaunchKernelGGL(sort_scan_kernel, dim3(args.total_batches), dim3(256), lds, stream, args);
     hipLaunchKernelGGL(sort_place_kernel, dim3(args.total_blocks), dim3(64), lds, stream, args);

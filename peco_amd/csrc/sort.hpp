@@ -17,9 +17,11 @@ struct SortProblem {
     int32_t* counts;        // nullable [batch, clusters]
     int32_t* offsets;       // [batch, clusters + 1]: first sorted position of each cluster
     int32_t* tile_hist;     // workspace [batch, tiles, clusters]
+    int32_t* next_hist;     // nullable, fused sort only: histograms cleared for the next producer
     int batch, tokens, clusters, tiles;
     int block_begin;        // first linear (batch, tile) block of this problem
     int batch_begin;        // first linear batch entry of this problem (scan grid)
+    int group_begin;        // first linear (batch, tile group) workgroup (fused grid)
 };
 
 constexpr int kMaxSortProblems = 2;
@@ -30,7 +32,20 @@ struct SortArgs {
     int total_blocks;   // sum of batch * tiles
     int total_batches;  // sum of batch
     int zero_hist;      // sort_place clears each consumed tile histogram (for accumulating producers)
+    int fused;          // one sort_fused launch instead of scan + place (sort_fusable problems only)
+    int total_groups;   // sum of batch * ceil(tiles / kFusedTiles)
 };
+
+// Fused sort: a workgroup ranks kFusedTiles consecutive tiles (one per wavefront) and derives
+// the cluster offsets of its batch entry from the tile histograms itself. Each workgroup reads
+// the whole [tiles, clusters] histogram of its entry, so this is for small entries only.
+constexpr int kFusedTiles = 4;
+constexpr int kFusedMaxTiles = 32;
+constexpr int kFusedMaxClusters = 1024;
+
+inline bool sort_fusable(int tokens, int clusters) {
+    return ceil_div(tokens, kSortTile) <= kFusedMaxTiles && clusters <= kFusedMaxClusters;
+}
 
 inline int sort_tiles(int tokens) { return static_cast<int>(ceil_div(tokens, kSortTile)); }
 
@@ -42,7 +57,9 @@ inline size_t sort_workspace_ints(int batch, int tokens, int clusters) {
 void sort_args_finalize(SortArgs& args);
 
 // with_hist=false: tile_hist already holds the per-tile label counts (e.g. accumulated
-// by the k-means assign kernel), so only the scan and place kernels run.
+// by the k-means assign kernel), so only the scan and place kernels run (or, with
+// args.fused, the single fused kernel, which leaves tile_hist unchanged and clears
+// next_hist instead).
 hipError_t launch_cluster_sort(const SortArgs& args, hipStream_t stream, bool with_hist);
 
 }  // namespace peco

@@ -171,6 +171,12 @@ def test_update_lockstep_fp32(announce, dims):
     (torch.float32, 128, 2048, 32, 32, 10),
     (torch.bfloat16, 128, 6750, 64, 256, 10),
     (torch.float16, 64, 3000, 20, 50, 6),
+    # Sort paths: one fused scan+place launch needs <= 32 tiles of 256 tokens and <= 1024
+    # clusters in every problem; otherwise separate scan and place launches run.
+    (torch.bfloat16, 64, 8192, 24, 96, 4),     # fused, exactly 32 tiles
+    (torch.bfloat16, 64, 4000, 10, 1000, 3),   # fused, clusters span four 256-thread passes
+    (torch.bfloat16, 64, 9000, 16, 40, 4),     # 36 tiles: scan + place
+    (torch.bfloat16, 64, 5000, 16, 1100, 3),   # 1100 clusters: scan + place
 ])
 def test_fused_fit_bit_exact(announce, dtype, dims, n, kq, kk, iters):
     g = _gen(n + kq)
