@@ -92,17 +92,17 @@ def stage_breakdown(layer, wl, q, k, v, q_init, k_init, reps):
         ql, kl, qs, ks = layer._update_cluster_state(q[:, :, :n], k[:, :, :n])
         q_idx, k_idx = layer._last_fit
         ev[1].record()
-        emap, eqs, eks = clustering_cuda.select_connections(
+        emap, eqs, eks, kept = clustering_cuda.select_connections(
             layer.q_centroids.reshape(1, heads, -1, dim), layer.k_centroids.reshape(1, heads, -1, dim), qs, ks,
-            wl.top_p, minimum, text=(s.text, s.text))
+            wl.top_p, minimum, text=(s.text, s.text), with_kept=True)
         ev[2].record()
         if s.bits == 0:
-            attn_args = (q, k, v, emap, eqs, eks, q_idx, k_idx, n)
+            attn_args = (q, k, v, emap, eqs, eks, q_idx, k_idx, n, kept)
         else:
             qp, kp, vp = clustering_cuda.pack_clustered([q, k, v], [q_idx, k_idx, k_idx], [ql, kl, None],
                                                         [layer.q_centroids, layer.k_centroids, None],
                                                         [s.bits, s.bits, 0], n)
-            attn_args = (qp, kp, vp, emap, eqs, eks, q_idx, None, n)
+            attn_args = (qp, kp, vp, emap, eqs, eks, q_idx, None, n, None)
         ev[3].record()
         run_attention(attn_args)
         ev[4].record()
@@ -117,12 +117,12 @@ def run_attention(args_):
     """The layer's attention launch: indexed inputs when k_index is given, else packed ones."""
     from peco_amd import attention_cuda
 
-    q, k, v, emap, eqs, eks, q_idx, k_idx, rows = args_
+    q, k, v, emap, eqs, eks, q_idx, k_idx, rows, kept = args_
     if k_idx is None:
         return attention_cuda.sparse_attention(q, k, v, emap, eqs, eks, validate_sizes=False, out_index=q_idx,
                                                out_index_rows=rows)
     return attention_cuda.sparse_attention_indexed(q, k, v, emap, eqs, eks, q_idx, k_idx, rows,
-                                                   validate_sizes=False)
+                                                   validate_sizes=False, kept_keys=kept)
 
 
 def attention_kernel_time(args_, reps=20):

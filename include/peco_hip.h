@@ -116,22 +116,27 @@ int peco_sparse_attention_ex(const void* q, const void* k, const void* v, const 
  * index_rows of head b reads query row q_index[b,j] and key/value row k_index[b,j], and output
  * row j is written to row q_index[b,j]; later rows (text) keep their position. Fuses the
  * gather of peco/clustering.py:112-125 (processor.py:143-149) and the restore of
- * clustering.py:128-136 (processor.py:153-156) into the attention launch. index_rows <= min(sq, sk). */
+ * clustering.py:128-136 (processor.py:153-156) into the attention launch. index_rows <= min(sq, sk).
+ * kept_keys (nullable) [bh, cq]: key rows kept by each query cluster, as
+ * peco_select_cluster_connections writes them; they only order the work items. */
 int peco_sparse_attention_indexed(const void* q, const void* k, const void* v, const uint8_t* selected,
                                   const int* q_sizes, const int* k_sizes, void* output, const int32_t* q_index,
-                                  const int32_t* k_index, int index_rows, int* workspace, size_t workspace_ints,
-                                  int bh, int sq, int sk, int d, int cq, int ck, int dtype, void* stream);
+                                  const int32_t* k_index, int index_rows, const int32_t* kept_keys, int* workspace,
+                                  size_t workspace_ints, int bh, int sq, int sk, int d, int cq, int ck, int dtype,
+                                  void* stream);
 
 /* Cluster-pair selection (replaces the torch ops of peco/clustering.py:140-186), one
  * wavefront per query-cluster row: count-weighted softmax of centroid scores, stable
  * descending order, keep while the preceding mass is < p (all when p == 1), at least
  * max(1, minimum) pairs, empty clusters never pair. qc [bh,cq,dims], kc [bh,ck,dims] fp32,
  * counts int32. With extend != 0 the map is [bh,cq+2,ck+2] with the valid-text/padding
- * groups of peco/processor.py:68-84 and ext_q/ext_k receive the extended sizes. */
+ * groups of peco/processor.py:68-84 and ext_q/ext_k receive the extended sizes. kept_keys
+ * (nullable) [bh, cq(+2)] receives the number of key rows each map row keeps (the cost of
+ * its query rows for the attention work list). */
 int peco_select_cluster_connections(const float* qc, const float* kc, const int32_t* q_counts,
                                     const int32_t* k_counts, int bh, int cq, int ck, int dims, float p, int minimum,
                                     int extend, int valid_text, int text, uint8_t* map, int32_t* ext_q,
-                                    int32_t* ext_k, void* stream);
+                                    int32_t* ext_k, int32_t* kept_keys, void* stream);
 
 #ifdef __cplusplus
 }

@@ -62,7 +62,7 @@ def _check_index(index, name, batch, heads, rows):
         raise ValueError(f"{name} must hold B*H*{rows} elements")
 
 
-def _launch(q, k, v, dynamic_map, q_sizes, k_sizes, validate_sizes, out_index, k_index, rows):
+def _launch(q, k, v, dynamic_map, q_sizes, k_sizes, validate_sizes, out_index, k_index, rows, kept_keys=None):
     batch, heads, sq, dim, sk, cq, ck, stride = _validate(q, k, v, dynamic_map, q_sizes, k_sizes)
     with torch.cuda.device(q.device):
         if not _device_is_gfx950(q.device):
@@ -86,11 +86,15 @@ def _launch(q, k, v, dynamic_map, q_sizes, k_sizes, validate_sizes, out_index, k
             _check_index(k_index, "k_index", batch, heads, rows)
             if k_index.device != q.device or out_index.device != q.device:
                 raise ValueError("All sparse attention inputs must reside on the same GPU device")
+        if kept_keys is not None:
+            _check_index(kept_keys, "kept_keys", batch, heads, cq)
+            if kept_keys.device != q.device:
+                raise ValueError("All sparse attention inputs must reside on the same GPU device")
         # Same footprint as the reference's workspace (peco/attention_cuda.py:112-113,128).
         workspace = torch.empty(batch * heads * stride, dtype=torch.int32, device=q.device)
         library = _native.library()
         stream = _native.current_stream(q.device, q, k, v, dynamic_map, q_sizes, k_sizes, workspace, output,
-                                        out_index, k_index)
+                                        out_index, k_index, kept_keys)
         dtype = 0 if q.dtype == torch.float16 else 1
         head = (_native.ptr(q), _native.ptr(k), _native.ptr(v), _native.ptr(dynamic_map), _native.ptr(q_sizes),
                 _native.ptr(k_sizes), _native.ptr(output))
@@ -100,7 +104,8 @@ def _launch(q, k, v, dynamic_map, q_sizes, k_sizes, validate_sizes, out_index, k
                                                      workspace.numel(), *tail)
         else:
             error = library.peco_sparse_attention_indexed(*head, _native.ptr(out_index), _native.ptr(k_index), rows,
-                                                          _native.ptr(workspace), workspace.numel(), *tail)
+                                                          _native.ptr(kept_keys), _native.ptr(workspace),
+                                                          workspace.numel(), *tail)
         if error:
             message = library.peco_attention_error_string(error).decode("utf-8", errors="replace")
             raise RuntimeError(f"PECO HIP sparse attention launch failed: {message} ({error})")
@@ -144,6 +149,7 @@ def sparse_attention_indexed(
     index_rows: int,
     *,
     validate_sizes: bool = True,
+    kept_keys: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """``sparse_attention`` on Q/K/V left in their original token order.
 
@@ -154,7 +160,9 @@ def sparse_attention_indexed(
     ``sparse_attention(gather(q, q_index), gather(k, k_index), gather(v, k_index), ...,
     out_index=q_index, out_index_rows=R)`` bit for bit, without the gather pass
     (peco/processor.py:143-156 with the reorder of peco/clustering.py:112-136 fused in).
+    ``kept_keys`` (int32 [B,H,CQ], optional) gives the key rows each query cluster keeps, as
+    ``select_connections(..., with_kept=True)`` returns them; it only orders the work items.
     """
     if q_index is None or k_index is None:
         raise ValueError("q_index and k_index are required")
-    return _launch(q, k, v, dynamic_map, q_sizes, k_sizes, validate_sizes, q_index, k_index, index_rows)
+    return _launch(q, k, v, dynamic_map, q_sizes, k_sizes, validate_sizes, q_index, k_index, index_rows, kept_keys)

@@ -170,12 +170,14 @@ def kmeans_fit(problems, iterations):
     return outs
 
 
-def select_connections(query_centroids, key_centroids, q_counts, k_counts, p, minimum, text=None):
+def select_connections(query_centroids, key_centroids, q_counts, k_counts, p, minimum, text=None, *,
+                       with_kept=False):
     """Cluster-pair map of select_cluster_connections in one launch.
 
     Centroids [..., C, D], counts [..., C]. With ``text=(valid_text, text_length)`` the map
     is extended with the text partition and the extended size vectors are returned too.
-    Returns (map bool [..., CQ(+2), CK(+2)], ext_q_sizes or None, ext_k_sizes or None).
+    Returns (map bool [..., CQ(+2), CK(+2)], ext_q_sizes or None, ext_k_sizes or None), and
+    with ``with_kept`` also int32 [..., CQ(+2)]: the key rows each map row keeps.
     """
     library = _library()
     lead = query_centroids.shape[:-2]
@@ -194,14 +196,18 @@ def select_connections(query_centroids, key_centroids, q_counts, k_counts, p, mi
     dmap = torch.empty((*lead, re, ce), dtype=torch.bool, device=dev)
     ext_q = torch.empty((*lead, re), dtype=torch.int32, device=dev) if extend else None
     ext_k = torch.empty((*lead, ce), dtype=torch.int32, device=dev) if extend else None
+    kept = torch.empty((*lead, re), dtype=torch.int32, device=dev) if with_kept else None
     valid_text, text_length = text if extend else (0, 0)
     with torch.cuda.device(dev):
         status = library.peco_select_cluster_connections(
             _native.ptr(qc), _native.ptr(kc), _native.ptr(qn), _native.ptr(kn), bh, cq, ck, dims, float(p),
             int(minimum), int(extend), int(valid_text), int(text_length), _native.ptr(dmap), _native.ptr(ext_q),
-            _native.ptr(ext_k), _retain_on_current_stream(dev, qc, kc, qn, kn, dmap, ext_q, ext_k),
+            _native.ptr(ext_k), _native.ptr(kept), _retain_on_current_stream(dev, qc, kc, qn, kn, dmap, ext_q, ext_k,
+                                                                             kept),
         )
     _raise_cluster_error(status)
+    if with_kept:
+        return dmap, ext_q, ext_k, kept
     return dmap, ext_q, ext_k
 
 

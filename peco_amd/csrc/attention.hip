@@ -84,85 +84,156 @@ __device__ __forceinline__ int block_scan256(int v, int* tmp, int* total) {
     return base + inc - v;
 }
 
+// Map rows read per wavefront per pass, and bytes of a row per lane per pass (320 keys): one
+// pass covers a head of up to 96 query clusters and 320 key clusters.
+constexpr int kMapRows = 24;
+constexpr int kMapU = 5;
+// Sort payload: query cluster (high bits) and item index within the cluster (low kItemBits).
+constexpr int kItemBits = 12;
+
+// kGivenKept: kept_in [bh, cq] holds each query cluster's kept key rows (from the selection
+// launch), so the map is not read; the counts only order the items.
+template <bool kGivenKept>
 __global__ __launch_bounds__(256) void build_work_kernel(const uint8_t* __restrict__ selected,
                                                          const int* __restrict__ q_sizes,
-                                                         const int* __restrict__ k_sizes, int32_t* ws, int bhn,
+                                                         const int* __restrict__ k_sizes,
+                                                         const int32_t* __restrict__ kept_in, int32_t* ws, int bhn,
                                                          int sq, int sk, int cq, int ck) {
     extern __shared__ int lds[];
     __shared__ int tmp[4];
     const int bh = blockIdx.x;
+    const int wave = threadIdx.x / kWave, lane = lane_id();
     WorkLayout W = work_layout(ws, bhn, sq, cq, ck);
     int* ksz = lds;              // [ck] clamped key cluster sizes
     int* qoff = ksz + ck;        // [cq + 1] clamped query offsets
     int* kept = qoff + cq + 1;   // [cq] kept keys per query cluster
     uint64_t* keys = reinterpret_cast<uint64_t*>(lds + ((ck + 2 * cq + 1 + 1) & ~1));  // [pow2 >= cap] sort keys
     int32_t* kpre = W.kprefix + static_cast<int64_t>(bh) * (ck + 1);
+    const uint8_t* map = selected + static_cast<int64_t>(bh) * cq * ck;
+    // The map rows of wavefront w are w, w+4, ...; a pass covers kMapRows of them and kMapU*64
+    // keys, every byte load of the pass in flight at once. The first pass is issued before the
+    // size scans so its latency overlaps them.
+    const int my_rows = cq > wave ? static_cast<int>(ceil_div(cq - wave, 4)) : 0;
+    const int chunks = static_cast<int>(ceil_div(ck, kMapU * kWave));
+    const int passes = kGivenKept ? 0 : static_cast<int>(ceil_div(my_rows, kMapRows)) * chunks;
+    // Raw bytes, kept unmasked so that the loads stay in flight until the pass uses them: a
+    // clamped duplicate row (past my_rows) is never written back, a clamped column (past ck)
+    // meets a zero size.
+    int m[kMapRows][kMapU];
+    auto issue = [&](int pass) {
+        const int r0 = (pass / chunks) * kMapRows;
+        const int k0 = (pass % chunks) * kMapU * kWave;
+#pragma unroll
+        for (int r = 0; r < kMapRows; ++r) {
+            const int c = min(wave + 4 * max(0, min(r0 + r, my_rows - 1)), cq - 1);
+            const uint8_t* row = map + static_cast<int64_t>(c) * ck;
+#pragma unroll
+            for (int u = 0; u < kMapU; ++u) m[r][u] = row[min(k0 + u * kWave + lane, ck - 1)];
+        }
+    };
+    // Cluster sizes: up to kSizes per thread are loaded together (clamped, masked after). They
+    // are issued before the first map pass: loads complete in order, so the size scans below
+    // then wait only for these.
+    constexpr int kSizes = 4;
+    const int kper = static_cast<int>(ceil_div(ck, 256));
+    const int qper = static_cast<int>(ceil_div(cq, 256));
+    int kv[kSizes], qv[kSizes];
+    if (kper <= kSizes && qper <= kSizes) {
+#pragma unroll
+        for (int i = 0; i < kSizes; ++i) {
+            kv[i] = k_sizes[static_cast<int64_t>(bh) * ck + min(static_cast<int>(threadIdx.x) * kper + i, ck - 1)];
+            qv[i] = q_sizes[static_cast<int64_t>(bh) * cq + min(static_cast<int>(threadIdx.x) * qper + i, cq - 1)];
+        }
+    }
+    if constexpr (!kGivenKept) issue(0);  // unconditional (rows clamped): later waits count these loads exactly
+    for (int c = threadIdx.x; c < cq; c += blockDim.x)
+        kept[c] = kGivenKept ? max(0, kept_in[static_cast<int64_t>(bh) * cq + c]) : 0;
     // Key cluster offsets: min(sk, prefix of max(0, size)).
     {
-        const int per = static_cast<int>(ceil_div(ck, 256));
+        const int per = kper;
         const int c0 = threadIdx.x * per, c1 = min(ck, c0 + per);
         int local = 0;
-        for (int c = c0; c < c1; ++c) local += max(0, k_sizes[static_cast<int64_t>(bh) * ck + c]);
+        if (kper <= kSizes && qper <= kSizes) {
+#pragma unroll
+            for (int i = 0; i < kSizes; ++i) {
+                if (c0 + i < c1) {
+                    ksz[c0 + i] = max(0, kv[i]);
+                    local += max(0, kv[i]);
+                }
+            }
+        } else {
+            for (int c = c0; c < c1; ++c) {
+                const int v = max(0, k_sizes[static_cast<int64_t>(bh) * ck + c]);
+                ksz[c] = v;
+                local += v;
+            }
+        }
         int total;
         int run = block_scan256(local, tmp, &total);
         for (int c = c0; c < c1; ++c) {
             const int a = min(sk, run);
-            run += max(0, k_sizes[static_cast<int64_t>(bh) * ck + c]);
+            run += ksz[c];
             const int e = min(sk, run);
             kpre[c] = a;
             ksz[c] = e - a;
         }
         if (threadIdx.x == 0) kpre[ck] = min(sk, total);
     }
-    // Query cluster offsets.
+    // Query cluster offsets (qoff[c] holds the clamped size until the scan replaces it).
     {
-        const int per = static_cast<int>(ceil_div(cq, 256));
+        const int per = qper;
         const int c0 = threadIdx.x * per, c1 = min(cq, c0 + per);
         int local = 0;
-        for (int c = c0; c < c1; ++c) local += max(0, q_sizes[static_cast<int64_t>(bh) * cq + c]);
+        if (kper <= kSizes && qper <= kSizes) {
+#pragma unroll
+            for (int i = 0; i < kSizes; ++i) {
+                if (c0 + i < c1) {
+                    qoff[c0 + i] = max(0, qv[i]);
+                    local += max(0, qv[i]);
+                }
+            }
+        } else {
+            for (int c = c0; c < c1; ++c) {
+                const int v = max(0, q_sizes[static_cast<int64_t>(bh) * cq + c]);
+                qoff[c] = v;
+                local += v;
+            }
+        }
         int total;
         int run = block_scan256(local, tmp, &total);
         for (int c = c0; c < c1; ++c) {
+            const int v = qoff[c];
             qoff[c] = min(sq, run);
-            run += max(0, q_sizes[static_cast<int64_t>(bh) * cq + c]);
+            run += v;
         }
         if (threadIdx.x == 0) qoff[cq] = min(sq, total);
     }
     __syncthreads();
-    // Kept keys per query cluster: one wave per map row, two rows per pass, each row's bytes
-    // read with all of a pass's loads (8 per row and lane) in flight at once.
-    {
-        const int wave = threadIdx.x / kWave, lane = lane_id();
-        constexpr int kU = 8;
-        for (int c0 = wave; c0 < cq; c0 += 8) {
-            int sum[2] = {0, 0};
-            for (int k0 = 0; k0 < ck; k0 += kU * kWave) {
-                uint8_t m[2][kU];
+    // Kept keys per query cluster: each pass adds its rows' chunk sums (a row is only ever
+    // touched by its own wavefront, so the read-modify-write needs no atomics).
+    for (int pass = 0; pass < passes; ++pass) {
+        const int r0 = (pass / chunks) * kMapRows;
+        const int k0 = (pass % chunks) * kMapU * kWave;
+        int w[kMapU];  // sizes of this lane's key clusters in the chunk (0 past ck)
 #pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    const int c = c0 + 4 * t;
-                    const uint8_t* row = selected + (static_cast<int64_t>(bh) * cq + min(c, cq - 1)) * ck;
+        for (int u = 0; u < kMapU; ++u) {
+            const int kc = k0 + u * kWave + lane;
+            const int v = ksz[min(kc, ck - 1)];
+            w[u] = kc < ck ? v : 0;
+        }
+        int sum[kMapRows];
 #pragma unroll
-                    for (int u = 0; u < kU; ++u) {
-                        // Unconditional load (clamped index), masked after: a guarded load
-                        // would wait for each byte before issuing the next.
-                        const int kc = k0 + u * kWave + lane;
-                        const uint8_t v = row[min(kc, ck - 1)];
-                        m[t][u] = (c < cq && kc < ck) ? v : 0;
-                    }
-                }
+        for (int r = 0; r < kMapRows; ++r) {
+            sum[r] = 0;
 #pragma unroll
-                for (int t = 0; t < 2; ++t)
+            for (int u = 0; u < kMapU; ++u) sum[r] += (m[r][u] & 0xff) ? w[u] : 0;
+        }
+        if (pass + 1 < passes) issue(pass + 1);
 #pragma unroll
-                    for (int u = 0; u < kU; ++u)
-                        if (m[t][u]) sum[t] += ksz[k0 + u * kWave + lane];
-            }
+        for (int r = 0; r < kMapRows; ++r) {
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-#pragma unroll
-                for (int m = 1; m < kWave; m <<= 1) sum[t] += __shfl_xor(sum[t], m, kWave);
-                if (lane == 0 && c0 + 4 * t < cq) kept[c0 + 4 * t] = sum[t];
-            }
+            for (int o = 1; o < kWave; o <<= 1) sum[r] += __shfl_xor(sum[r], o, kWave);
+            if (lane == 0 && r0 + r < my_rows) kept[wave + 4 * (r0 + r)] += sum[r];
         }
     }
     __syncthreads();
@@ -170,27 +241,56 @@ __global__ __launch_bounds__(256) void build_work_kernel(const uint8_t* __restri
     const int per = static_cast<int>(ceil_div(cq, 256));
     const int c0 = threadIdx.x * per, c1 = min(cq, c0 + per);
     int local = 0;
-    for (int c = c0; c < c1; ++c) local += static_cast<int>(ceil_div(qoff[c + 1] - qoff[c], kQTile));
+    bool fits = true;  // every item is addressable by the sort payload
+    for (int c = c0; c < c1; ++c) {
+        const int n = static_cast<int>(ceil_div(qoff[c + 1] - qoff[c], kQTile));
+        local += n;
+        fits = fits && n <= (1 << kItemBits);
+    }
     int count;
     int slot = block_scan256(local, tmp, &count);
+    const bool sortable = count <= kSortCap && __syncthreads_and(fits) && cq < (1 << (32 - kItemBits));
     int32_t* items = W.items + static_cast<int64_t>(bh) * W.cap * 3;
-    const bool sortable = count <= kSortCap;
+    if (threadIdx.x == 0) W.counts[bh] = count;
+    if (!sortable) {
+        // Cluster order, written directly.
+        for (int c = c0; c < c1; ++c) {
+            const int rows = qoff[c + 1] - qoff[c];
+            for (int r = 0; r < rows; r += kQTile, ++slot) {
+                items[3 * slot + 0] = qoff[c] + r;
+                items[3 * slot + 1] = c;
+                items[3 * slot + 2] = min(kQTile, rows - r);
+            }
+        }
+        return;
+    }
     for (int c = c0; c < c1; ++c) {
         const int rows = qoff[c + 1] - qoff[c];
-        for (int r = 0; r < rows; r += kQTile, ++slot) {
+        for (int r = 0, ri = 0; r < rows; r += kQTile, ++slot, ++ri) {
             const int n = min(kQTile, rows - r);
-            if (sortable) {
-                const uint32_t cost = static_cast<uint32_t>(min<int64_t>(static_cast<int64_t>(n) * kept[c], 0x7fffffff));
-                // Pack (descending cost, item payload index) for an ascending sort.
-                keys[slot] = (static_cast<uint64_t>(~cost) << 32) | static_cast<uint32_t>(slot);
-            }
-            items[3 * slot + 0] = qoff[c] + r;
-            items[3 * slot + 1] = c;
-            items[3 * slot + 2] = n;
+            const uint32_t cost = static_cast<uint32_t>(min<int64_t>(static_cast<int64_t>(n) * kept[c], 0x7fffffff));
+            // (descending cost, cluster, item) for an ascending sort; ties keep cluster order.
+            keys[slot] = (static_cast<uint64_t>(~cost) << 32) | (static_cast<uint32_t>(c) << kItemBits) |
+                         static_cast<uint32_t>(ri);
         }
     }
-    if (threadIdx.x == 0) W.counts[bh] = count;
-    if (!sortable || count <= 1) return;
+    __syncthreads();
+    if (count <= 256) {
+        // Rank sort: the keys are distinct, so each one's rank (the number of smaller keys) is
+        // its position. All threads read the same key at a time (LDS broadcast).
+        uint64_t mine = threadIdx.x < count ? keys[threadIdx.x] : ~0ull;
+        int rank = 0;
+        for (int j = 0; j < count; ++j) rank += keys[j] < mine ? 1 : 0;
+        if (threadIdx.x < count) {
+            const uint32_t payload = static_cast<uint32_t>(mine);
+            const int c = static_cast<int>(payload >> kItemBits);
+            const int r = static_cast<int>(payload & ((1u << kItemBits) - 1u)) * kQTile;
+            items[3 * rank + 0] = qoff[c] + r;
+            items[3 * rank + 1] = c;
+            items[3 * rank + 2] = min(kQTile, qoff[c + 1] - qoff[c] - r);
+        }
+        return;
+    }
     int n2 = 1;
     while (n2 < count) n2 <<= 1;
     for (int i = count + threadIdx.x; i < n2; i += 256) keys[i] = ~0ull;
@@ -211,21 +311,14 @@ __global__ __launch_bounds__(256) void build_work_kernel(const uint8_t* __restri
             __syncthreads();
         }
     }
-    // Permute items into cost order (read all, then write all).
-    int v[3 * 8];
-    int nmine = 0;
-    for (int i = threadIdx.x; i < count && nmine < 8; i += 256, ++nmine) {
-        const int src = static_cast<int>(keys[i] & 0xffffffffu);
-        v[3 * nmine + 0] = items[3 * src + 0];
-        v[3 * nmine + 1] = items[3 * src + 1];
-        v[3 * nmine + 2] = items[3 * src + 2];
-    }
-    __syncthreads();
-    nmine = 0;
-    for (int i = threadIdx.x; i < count && nmine < 8; i += 256, ++nmine) {
-        items[3 * i + 0] = v[3 * nmine + 0];
-        items[3 * i + 1] = v[3 * nmine + 1];
-        items[3 * i + 2] = v[3 * nmine + 2];
+    // Items in cost order, rebuilt from the payload.
+    for (int i = threadIdx.x; i < count; i += 256) {
+        const uint32_t payload = static_cast<uint32_t>(keys[i]);
+        const int c = static_cast<int>(payload >> kItemBits);
+        const int r = static_cast<int>(payload & ((1u << kItemBits) - 1u)) * kQTile;
+        items[3 * i + 0] = qoff[c] + r;
+        items[3 * i + 1] = c;
+        items[3 * i + 2] = min(kQTile, qoff[c + 1] - qoff[c] - r);
     }
 }
 
@@ -588,7 +681,8 @@ namespace {
 // token order, read through out_index for Q and k_index for K/V).
 int launch_sparse_attention(const void* q, const void* k, const void* v, const uint8_t* selected,
                             const int* q_sizes, const int* k_sizes, void* output, const int32_t* out_index,
-                            int out_index_rows, const int32_t* k_index, int* workspace, size_t workspace_ints,
+                            int out_index_rows, const int32_t* k_index, const int32_t* kept_keys, int* workspace,
+                            size_t workspace_ints,
                             int bh, int sq, int sk, int d, int cq, int ck, int dtype, void* stream) {
     if (!q || !k || !v || !selected || !q_sizes || !k_sizes || !output || !workspace || bh < 1 || bh > 65535 ||
         sq < 0 || sk < 0 || cq < 1 || ck < 1 || (d != 64 && d != 128) || (dtype != kF16 && dtype != kBF16) ||
@@ -601,8 +695,12 @@ int launch_sparse_attention(const void* q, const void* k, const void* v, const u
     const size_t lds_attn = sizeof(int) * (2 * static_cast<size_t>(ck) + 1);
     if (lds_build > 60 * 1024 || lds_attn > 24 * 1024) return kUnsupportedShape;
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(build_work_kernel, dim3(bh), dim3(256), lds_build, s, selected, q_sizes, k_sizes, workspace, bh,
-                       sq, sk, cq, ck);
+    if (kept_keys)
+        hipLaunchKernelGGL(build_work_kernel<true>, dim3(bh), dim3(256), lds_build, s, selected, q_sizes, k_sizes,
+                           kept_keys, workspace, bh, sq, sk, cq, ck);
+    else
+        hipLaunchKernelGGL(build_work_kernel<false>, dim3(bh), dim3(256), lds_build, s, selected, q_sizes, k_sizes,
+                           nullptr, workspace, bh, sq, sk, cq, ck);
     const int cap = item_capacity(sq, cq);
     const float scale_log2 = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(d)));
     const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(cap) * bh));
@@ -641,20 +739,22 @@ PECO_API int peco_sparse_attention_ex(const void* q, const void* k, const void* 
                                       int out_index_rows, int* workspace, size_t workspace_ints, int bh, int sq,
                                       int sk, int d, int cq, int ck, int dtype, void* stream) {
     return launch_sparse_attention(q, k, v, selected, q_sizes, k_sizes, output, out_index, out_index_rows, nullptr,
-                                   workspace, workspace_ints, bh, sq, sk, d, cq, ck, dtype, stream);
+                                   nullptr, workspace, workspace_ints, bh, sq, sk, d, cq, ck, dtype, stream);
 }
 
 // Gathering entry: q, k, v (and output) stay in original token order. The first index_rows
 // rows of each head are read in cluster order through q_index (queries, also the output
-// scatter) and k_index (keys and values), so no packed copies are needed.
+// scatter) and k_index (keys and values), so no packed copies are needed. kept_keys (nullable,
+// [bh, cq]) gives each query cluster's kept key rows, as the selection launch writes them;
+// the work-list builder then orders items without reading the map.
 PECO_API int peco_sparse_attention_indexed(const void* q, const void* k, const void* v, const uint8_t* selected,
                                            const int* q_sizes, const int* k_sizes, void* output,
                                            const int32_t* q_index, const int32_t* k_index, int index_rows,
-                                           int* workspace, size_t workspace_ints, int bh, int sq, int sk, int d,
-                                           int cq, int ck, int dtype, void* stream) {
+                                           const int32_t* kept_keys, int* workspace, size_t workspace_ints, int bh,
+                                           int sq, int sk, int d, int cq, int ck, int dtype, void* stream) {
     if (index_rows < 0 || (index_rows > 0 && (!q_index || !k_index))) return kInvalidValue;
     if (index_rows == 0) q_index = k_index = nullptr;  // nothing is permuted
-    return launch_sparse_attention(q, k, v, selected, q_sizes, k_sizes, output, q_index, index_rows, k_index,
+    return launch_sparse_attention(q, k, v, selected, q_sizes, k_sizes, output, q_index, index_rows, k_index, kept_keys,
                                    workspace, workspace_ints, bh, sq, sk, d, cq, ck, dtype, stream);
 }
 

@@ -54,7 +54,8 @@ template <int KPL>
 __global__ __launch_bounds__(kSelWaves * kWave) void select_kernel(
     const float* __restrict__ qc, const float* __restrict__ kc, const int32_t* __restrict__ qn,
     const int32_t* __restrict__ kn, int bh, int cq, int ck, int dims, float scale, float p, int minimum, int extend,
-    int valid_text, int text, uint8_t* __restrict__ map, int32_t* __restrict__ ext_q, int32_t* __restrict__ ext_k) {
+    int valid_text, int text, uint8_t* __restrict__ map, int32_t* __restrict__ ext_q, int32_t* __restrict__ ext_k,
+    int32_t* __restrict__ kept_keys) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int groups = static_cast<int>(ceil_div(cq, kSelWaves));
@@ -84,6 +85,18 @@ __global__ __launch_bounds__(kSelWaves * kWave) void select_kernel(
             ext_q[static_cast<int64_t>(b) * re + cq + 1] = text - valid_text;
             ext_k[static_cast<int64_t>(b) * ce + ck] = valid_text;
             ext_k[static_cast<int64_t>(b) * ce + ck + 1] = text - valid_text;
+        }
+        if (kept_keys) {
+            // The valid-text row sees every video key and the valid text; the padding row only
+            // the padding.
+            int all = 0;
+            for (int j = lane; j < ck; j += kWave) all += max(0, kn[static_cast<int64_t>(b) * ck + j]);
+#pragma unroll
+            for (int m = 1; m < kWave; m <<= 1) all += __shfl_xor(all, m, kWave);
+            if (lane == 0) {
+                kept_keys[static_cast<int64_t>(b) * re + cq] = all + valid_text;
+                kept_keys[static_cast<int64_t>(b) * re + cq + 1] = text - valid_text;
+            }
         }
     }
     for (int t = threadIdx.x; t < kSelWaves * dims; t += blockDim.x) {
@@ -252,13 +265,23 @@ __global__ __launch_bounds__(kSelWaves * kWave) void select_kernel(
         }
     }
     const bool qnonempty = qn[static_cast<int64_t>(b) * cq + c] > 0;
+    int kept_rows = 0;  // key rows behind this row's kept clusters
 #pragma unroll
     for (int e = 0; e < KPL; ++e) {
         const int k = lane * KPL + e;
         if (k < ck) {
             const int j = static_cast<int>(key[e] & 0xffffffffu);
-            flags[j] = k < kept && qnonempty && kcount[j] > 0;
+            const int n = kcount[j];
+            const bool on = k < kept && qnonempty && n > 0;
+            flags[j] = on;
+            kept_rows += on ? n : 0;
         }
+    }
+    if (kept_keys) {
+#pragma unroll
+        for (int m = 1; m < kWave; m <<= 1) kept_rows += __shfl_xor(kept_rows, m, kWave);
+        if (lane == 0)
+            kept_keys[static_cast<int64_t>(b) * re + c] = kept_rows + (extend ? valid_text : 0);  // as the map row
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -271,10 +294,10 @@ __global__ __launch_bounds__(kSelWaves * kWave) void select_kernel(
 template <int KPL>
 void launch_select(int blocks, size_t lds, hipStream_t stream, const float* qc, const float* kc, const int32_t* qn,
                    const int32_t* kn, int bh, int cq, int ck, int dims, float scale, float p, int minimum, int extend,
-                   int valid_text, int text, uint8_t* map, int32_t* ext_q, int32_t* ext_k) {
+                   int valid_text, int text, uint8_t* map, int32_t* ext_q, int32_t* ext_k, int32_t* kept_keys) {
     hipLaunchKernelGGL(select_kernel<KPL>, dim3(static_cast<unsigned>(blocks)), dim3(kSelWaves * kWave), lds, stream,
                        qc, kc, qn, kn, bh, cq, ck, dims, scale, p, minimum, extend, valid_text, text, map, ext_q,
-                       ext_k);
+                       ext_k, kept_keys);
 }
 
 }  // namespace
@@ -285,12 +308,13 @@ using namespace peco;
 // Selection of cluster pairs, optionally extended with the text partition.
 // qc [bh, cq, dims], kc [bh, ck, dims] fp32; q_counts [bh, cq], k_counts [bh, ck] int32.
 // map: bool [bh, cq(+2), ck(+2)]; ext_q/ext_k (extend only): int32 [bh, cq+2] / [bh, ck+2].
+// kept_keys (nullable): int32 [bh, cq(+2)], the number of key rows each map row keeps.
 // minimum = ceil(min_kc_ratio * ck) computed by the caller. ck <= 2048, dims <= 256; the LDS use
 // (8 query rows, a 64-row key block and 8 rows of ck flag bytes) must fit in 64 KiB.
 PECO_API int peco_select_cluster_connections(const float* qc, const float* kc, const int32_t* q_counts,
                                              const int32_t* k_counts, int bh, int cq, int ck, int dims, float p,
                                              int minimum, int extend, int valid_text, int text, uint8_t* map,
-                                             int32_t* ext_q, int32_t* ext_k, void* stream) {
+                                             int32_t* ext_q, int32_t* ext_k, int32_t* kept_keys, void* stream) {
     if (!qc || !kc || !q_counts || !k_counts || !map || bh < 1 || cq < 1 || ck < 1 || dims < 1 || dims > kSelMaxDims ||
         !(p >= 0.0f && p <= 1.0f) || minimum < 0 || (extend && (!ext_q || !ext_k || valid_text < 0 || valid_text > text)))
         return kInvalidValue;
@@ -305,7 +329,7 @@ PECO_API int peco_select_cluster_connections(const float* qc, const float* kc, c
     const int per_lane = static_cast<int>(ceil_div(ck, kWave));
 #define PECO_SELECT(K)                                                                                          \
     launch_select<K>(blocks, lds, s, qc, kc, q_counts, k_counts, bh, cq, ck, dims, scale, p, minimum, extend,  \
-                     valid_text, text, map, ext_q, ext_k)
+                     valid_text, text, map, ext_q, ext_k, kept_keys)
     if (per_lane <= 1) PECO_SELECT(1);
     else if (per_lane <= 2) PECO_SELECT(2);
     else if (per_lane <= 4) PECO_SELECT(4);

@@ -195,15 +195,16 @@ class PecoAttention:
         q_idx, k_idx = self._last_fit
         # Cluster connectivity from the floating-point centres, extended with the text
         # partition (select_cluster_connections + extend_text_partition in one launch).
-        dynamic_map, q_sizes, k_sizes = clustering_cuda.select_connections(
+        dynamic_map, q_sizes, k_sizes, kept = clustering_cuda.select_connections(
             self.q_centroids.reshape(batch, heads, -1, dim), self.k_centroids.reshape(batch, heads, -1, dim),
             q_sizes, k_sizes, self.config.top_p,
-            math.ceil(self.config.min_kc_ratio * self.config.num_k_centroids), text=(valid_text, text_length))
+            math.ceil(self.config.min_kc_ratio * self.config.num_k_centroids), text=(valid_text, text_length),
+            with_kept=True)
         if bits == 0:
             # No fake quantization: attention reads Q/K/V through the sort permutations and
             # writes the output in original order, so no packed copy is made.
             return sparse_attention_indexed(query, key, value, dynamic_map, q_sizes, k_sizes, q_idx, k_idx,
-                                            video_length, validate_sizes=False)
+                                            video_length, validate_sizes=False, kept_keys=kept)
         # Fake-quantize Q/K against their centroids while packing Q/K/V into cluster order.
         q_perm, k_perm, v_perm = clustering_cuda.pack_clustered(
             [query, key, value], [q_idx, k_idx, k_idx], [q_labels, k_labels, None],

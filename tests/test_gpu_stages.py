@@ -351,6 +351,10 @@ def test_sparse_attention_indexed_equals_packed(announce, dtype, dims, sq, sk, r
                                              _gather_rows(dev[2], dev[7]), *dev[3:6], out_index=dev[6],
                                              out_index_rows=rows)
     assert torch.equal(indexed.cpu().view(torch.int16), packed.cpu().view(torch.int16))
+    # Kept-key counts only order the work items: any counts give the same bits.
+    kept = torch.randint(0, 5000, (1, h, cq), generator=g, dtype=torch.int32)
+    ordered = attention_cuda.sparse_attention_indexed(*dev[:6], dev[6], dev[7], rows, kept_keys=kept.to(DEV))
+    assert torch.equal(ordered.cpu().view(torch.int16), indexed.cpu().view(torch.int16))
     # And against the oracle on the packed inputs, restored to original order.
     pq, pk, pv = (_gather_rows(x, i)[0].float().numpy() for x, i in ((q, qi), (k, ki), (v, ki)))
     ref = canonical.sparse_attention(pq, pk, pv, m[0].numpy(), qs[0].numpy(), ks[0].numpy())
@@ -386,8 +390,11 @@ def test_select_with_text_partition_matches_oracle(announce):
     qs = torch.randint(1, 30, (1, 2, 16), generator=g, dtype=torch.int32)
     ks = torch.randint(0, 30, (1, 2, 40), generator=g, dtype=torch.int32)
     announce()
-    m, eq, ek = clustering_cuda.select_connections(qc.to(DEV), kc.to(DEV), qs.to(DEV), ks.to(DEV), 1e-9, 10,
-                                                   text=(7, 9))
+    m, eq, ek, kept = clustering_cuda.select_connections(qc.to(DEV), kc.to(DEV), qs.to(DEV), ks.to(DEV), 1e-9, 10,
+                                                         text=(7, 9), with_kept=True)
     rm, rq, rk = reference_path.extend_text_partition(
         reference_path.select_connections(qc, kc, qs, ks, 1e-9, 0.25), qs, ks, 7, 9)
     assert torch.equal(m.cpu(), rm) and torch.equal(eq.cpu(), rq) and torch.equal(ek.cpu(), rk)
+    # Kept key rows of every (extended) map row: the sizes of its kept columns.
+    ref_kept = (rm.to(torch.int64) * rk[:, :, None, :].to(torch.int64)).sum(-1).to(torch.int32)
+    assert torch.equal(kept.cpu(), ref_kept)
