@@ -35,6 +35,8 @@ namespace {
 constexpr int kQTile = 128;   // query rows per item (4 waves x 32)
 constexpr int kKTile = 64;    // keys per LDS tile
 constexpr int kSortCap = 2048;
+constexpr int kSplitRows = 64;  // items up to this many rows run in the paired-wave launch
+constexpr int kGallop = 8;      // key-stream segments a row lookup examines at once
 
 struct WorkLayout {
     int32_t* counts;   // [bh]
@@ -382,31 +384,48 @@ __device__ __forceinline__ void dma16(const uint16_t* src, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
 }
 
-// Issue the direct-to-LDS loads of one K and one V tile (no wait). Rows past the stream end
-// read row 0 of the head: their K scores are masked to -inf and their P is 0.
-template <int D>
+// The same with 4 bytes per lane: lane i writes lds + 4i.
+__device__ __forceinline__ void dma4(const void* src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p)));
+}
+
+// Issue the direct-to-LDS loads of one K and one V tile (no wait), or the share of a wave
+// that is one of NL loaders (rank `first`): the tile's 4*kLoads spans of 64 lanes x 16 bytes
+// per tensor go round-robin to the loaders. Rows past the stream end read row 0 of the head:
+// their K scores are masked to -inf and their P is 0.
+template <int D, int NL>
 __device__ __forceinline__ void load_tile_lds(uint16_t* ks, uint16_t* vs, const uint16_t* kh, const uint16_t* vh,
-                                              const int* prow, int wave, int lane) {
+                                              const int* prow, int first, int lane) {
 #if defined(__HIP_DEVICE_COMPILE__)
     using T = Tiles<D>;
-    int rows[T::kLoads];
-#pragma unroll
-    for (int i = 0; i < T::kLoads; ++i) rows[i] = prow[(i * 4 + wave) * T::kWaveRows + lane / T::CH];
-    // LDS byte address of this wave's first span in the K tile (wave-uniform) and the distance
+    constexpr int kSpans = 4 * T::kLoads / NL;  // spans per tensor for this loader
+    constexpr int kGroup = kSpans < 4 ? kSpans : 4;  // spans whose rows are read at once
+    // LDS byte address of this loader's first span in the K tile (wave-uniform) and the distance
     // from a K span to the matching V span.
     const uint32_t lds_base = __builtin_amdgcn_readfirstlane(
-        static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ks + wave * kWave * 8)));
+        static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ks + first * kWave * 8)));
     const uint32_t vs_delta = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(
         reinterpret_cast<uintptr_t>(vs) - reinterpret_cast<uintptr_t>(ks)));
+#pragma unroll 1
+    for (int i0 = 0; i0 < kSpans; i0 += kGroup) {
+        int rows[kGroup];
 #pragma unroll
-    for (int i = 0; i < T::kLoads; ++i) {
-        const int r = (i * 4 + wave) * T::kWaveRows + lane / T::CH;  // tile row written by this lane
-        const int p = lane % T::CH;                                      // physical chunk
-        const int64_t g = static_cast<int64_t>(rows[i]) * D;
-        const uint32_t kdst = lds_base + static_cast<uint32_t>(((i * 4) * kWave * 8) * 2);
-        const uint32_t vdst = kdst + vs_delta;
-        dma16(kh + g + (p ^ T::swz_k(r)) * 8, kdst);
-        dma16(vh + g + (p ^ T::swz_v(r)) * 8, vdst);
+        for (int j = 0; j < kGroup; ++j) rows[j] = prow[((i0 + j) * NL + first) * T::kWaveRows + lane / T::CH];
+#pragma unroll
+        for (int j = 0; j < kGroup; ++j) {
+            const int i = i0 + j;
+            const int r = (i * NL + first) * T::kWaveRows + lane / T::CH;  // tile row written by this lane
+            const int p = lane % T::CH;                                        // physical chunk
+            const int64_t g = static_cast<int64_t>(rows[j]) * D;
+            const uint32_t kdst = lds_base + static_cast<uint32_t>(((i * NL) * kWave * 8) * 2);
+            const uint32_t vdst = kdst + vs_delta;
+            dma16(kh + g + (p ^ T::swz_k(r)) * 8, kdst);
+            dma16(vh + g + (p ^ T::swz_v(r)) * 8, vdst);
+        }
     }
 #endif
 }
@@ -416,7 +435,7 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 // kIndexed: the inputs are in their original token order. Query row j < oi_rows of a head is
 // read from row out_index[j] (the same permutation that scatters the output) and key/value
 // stream row p < oi_rows from row k_index[p]; rows past oi_rows (text) keep their position.
-template <int DT, int D, bool kIndexed>
+template <int DT, int D, bool kIndexed, bool kSplit>
 __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint8_t* __restrict__ selected, const int32_t* __restrict__ ws, uint16_t* __restrict__ out,
@@ -430,12 +449,13 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     __shared__ __align__(16) uint16_t ks[2][T::kElems];
     __shared__ __align__(16) uint16_t vs[2][T::kElems];
     __shared__ int prow[2][kKTile];
+    __shared__ int pidx[2][kKTile];    // k_index values of tile t+3 rows (indexed inputs)
     __shared__ int tmp[4];
     extern __shared__ int dyn[];
-    // Key stream of this query cluster: the kept, non-empty key clusters in order. kst[i] is
-    // the first physical key row of the i-th of them, kof[i] its offset in the stream.
-    int* kst = dyn;             // [ck]
-    int* kof = dyn + ck;        // [ck + 1]
+    // Key stream of this query cluster: the kept, non-empty key clusters in order. Segment i
+    // is {first physical row - stream offset, stream offset} of the i-th of them, followed by
+    // kGallop + 1 sentinels whose offset no stream row reaches.
+    int2* kseg = reinterpret_cast<int2*>(dyn);  // [ck + 1 + kGallop]
 
     const int bh = blockIdx.x % bhn;
     const int slot = blockIdx.x / bhn;
@@ -443,6 +463,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     if (slot >= W.counts[bh]) return;
     const int32_t* item = W.items + (static_cast<int64_t>(bh) * W.cap + slot) * 3;
     const int q_start = item[0], qc = item[1], q_rows = item[2];
+    if ((q_rows <= kSplitRows) != kSplit) return;  // the other launch's item
     const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave, h = lane / 32;
 
     const uint8_t* sel = selected + (static_cast<int64_t>(bh) * cq + qc) * ck;
@@ -464,46 +485,89 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
         for (int c = c0; c < c1; ++c) {
             const int a = gk[c], e = gk[c + 1];
             if (sel[c] && e > a) {
-                kst[idx] = a;
-                kof[idx] = run;
+                kseg[idx] = int2{a - run, run};
                 ++idx;
                 run += e - a;
             }
         }
-        if (tid == 0) kof[nk] = L;
+        if (tid <= kGallop) kseg[nk + tid] = int2{0, 0x7fffffff};
     }
     __syncthreads();
     const int ntiles = static_cast<int>(ceil_div(L, kKTile));
-    // Physical row of stream row r (r < L). Each of threads 0..63 asks for increasing rows
-    // (its row of every tile), so a forward-only cursor over the kept clusters suffices.
+    // Physical row of stream row r (r < L). Every lane asks for increasing rows (its row of
+    // every tile), so a forward-only cursor over the segments suffices. The next kGallop
+    // segment offsets are read at once (independent LDS reads, no loop) and the ones <= r
+    // counted; only a jump over more segments than that continues one at a time.
     int cur = 0;
     auto row_of = [&](int r) {
-        while (cur + 1 < nk && kof[cur + 1] <= r) ++cur;
-        return kst[cur] + (r - kof[cur]);
+        int2 seg[kGallop + 1];
+#pragma unroll
+        for (int j = 0; j <= kGallop; ++j) seg[j] = kseg[cur + j];
+        int adv = 0;
+#pragma unroll
+        for (int j = 1; j <= kGallop; ++j) adv += seg[j].y <= r ? 1 : 0;
+        int delta = seg[0].x;
+#pragma unroll
+        for (int j = 1; j <= kGallop; ++j) delta = adv >= j ? seg[j].x : delta;
+        cur += adv;
+        if (adv == kGallop) {
+            while (kseg[cur + 1].y <= r) ++cur;
+            delta = kseg[cur].x;
+        }
+        return r + delta;
     };
-    // Indexed inputs: lanes 0..15 of every wave own the tile rows 16*wave + lane, so the index
-    // loads are spread over the waves. The indices of tile t+2 are loaded when tile t starts and
-    // written to prow at its end, so their latency hides behind tile t's MFMAs.
+    // Tile rows move through a pipeline. Lane l of wave w follows tile row 16*w + l%16 (lanes
+    // 0..15 own it, the others shadow it). During tile t it
+    //   - asks for the physical row of tile t+3 (indexed inputs: its k_index value is loaded
+    //     straight into pidx),
+    //   - issues the direct-to-LDS loads of tile t+1 (rows in prow, written a tile earlier)
+    //     right after its S^T MFMAs,
+    // and at the end it publishes its tile t+2 row in prow. Every load of the loop goes
+    // straight to LDS (no register is written behind the compiler's back), so the loop
+    // waits for them explicitly.
     const int64_t head = static_cast<int64_t>(bh);
     const int32_t* kidx = kIndexed ? k_index + head * oi_rows : nullptr;
     const uint32_t sq_last = static_cast<uint32_t>(sq - 1), sk_last = static_cast<uint32_t>(sk - 1);
-    const bool prow_owner = kIndexed ? lane < 16 : tid < kKTile;
-    const int prow_entry = kIndexed ? 16 * wave + lane : tid;
+    const int prow_entry = 16 * wave + lane % 16;
+    const bool prow_owner = lane < 16;
+    // Stream position (cluster-order row) of stream row r; rows past the stream read row 0.
+    auto stream_pos = [&](int r) { return r < L ? row_of(r) : 0; };
+    // Physical row of stream position p, given k_index[p] (clamped to the head's rows, so a bad
+    // permutation cannot read out of bounds).
+    auto physical = [&](int p, int raw) {
+        if constexpr (kIndexed) return p < oi_rows ? static_cast<int>(min(static_cast<uint32_t>(raw), sk_last)) : p;
+        else return p;
+    };
     auto stream_row = [&](int r) {
-        const int p = r < L ? row_of(r) : 0;
-        // Index values are clamped to the head's rows, so a bad permutation cannot read out of bounds.
-        if constexpr (kIndexed) return p < oi_rows ? static_cast<int>(min(static_cast<uint32_t>(kidx[p]), sk_last)) : p;
+        const int p = stream_pos(r);
+        if constexpr (kIndexed) return physical(p, kidx[min(p, oi_rows - 1)]);
         else return p;
     };
     if (prow_owner) {
         prow[0][prow_entry] = stream_row(prow_entry);
         prow[1][prow_entry] = stream_row(kKTile + prow_entry);
     }
+    int row2 = stream_row(2 * kKTile + prow_entry);  // this lane's row of tile t+2
 
-    // Q^T operand: lane holds query row (32*wave + l%32), channels 16s + 8h .. +7.
-    const int qrow = wave * 32 + (lane % 32);
+    // kSplit (items of at most kSplitRows rows) pairs the waves: wave w takes 32-row block
+    // w & 1 and, of every tile, only the 32-key half w >> 1, so a short item's tiles cost half
+    // the time; each pair merges its two partial softmax states after the last tile. Longer
+    // items give each wave its own row block and both halves of every tile.
+    const int rb = kSplit ? (wave & 1) : wave;  // this wave's 32-row block
+    const int hb = kSplit ? (wave >> 1) : 0;    // first 32-key half this wave processes
+    // Waves without query rows issue every tile load, so that waiting for the load path to
+    // accept them never delays a wave with MFMA work; with no such wave all four share.
+    const int row_blocks = static_cast<int>(ceil_div(q_rows, 32));
+    const int idle = kSplit ? 4 - 2 * row_blocks : 4 - row_blocks;   // waves 4-idle .. 3 (or 1, 3)
+    const int loaders = idle >= 2 ? 2 : (idle == 1 ? 1 : 4);
+    int loader_rank;
+    if (loaders == 4) loader_rank = wave;
+    else if constexpr (kSplit) loader_rank = (wave & 1) ? wave >> 1 : -1;   // idle waves 1 and 3
+    else loader_rank = wave >= 4 - loaders ? wave - (4 - loaders) : -1;
+    // Q^T operand: lane holds query row (32*rb + l%32), channels 16s + 8h .. +7.
+    const int qrow = rb * 32 + (lane % 32);
     const bool qvalid = qrow < q_rows;
-    const bool wave_active = wave * 32 < q_rows;
+    const bool wave_active = rb * 32 < q_rows;
     int64_t qsrc = q_start + qrow;
     if constexpr (kIndexed) {
         if (qvalid && qsrc < oi_rows) qsrc = min(static_cast<uint32_t>(out_index[head * oi_rows + qsrc]), sq_last);
@@ -526,117 +590,170 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     const int arow = lane % 32;                 // S^T A row (key within a 32-key block)
     const int gsub = (lane / 16) % 2;           // 16-lane group parity (V^T channel half)
     const int src = lane % 16;                  // source lane of the transpose read
+    // S^T, online softmax and O^T += V^T P^T for NCB consecutive 32-key halves of the tile in
+    // (kt, vt), starting at half cb0.
+    // after_s() runs once the S^T MFMAs are issued (the next tile's loads go there, so the
+    // wait for the load path to accept them overlaps the MFMAs).
+    auto compute = [&](auto ncbc, int cb0, const uint16_t* kt, const uint16_t* vt, int base, auto&& after_s)
+                       __attribute__((always_inline)) {
+        constexpr int NCB = decltype(ncbc)::value;
+        const bool partial = base + kKTile > L;
+        // S^T for all halves first, so the softmax of one half overlaps MFMAs.
+        f32x16 sacc[NCB];
+#pragma unroll
+        for (int j = 0; j < NCB; ++j) {
+            sacc[j] = f32x16{};
+            const int krow = 32 * (cb0 + j) + arow;
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const int pc = (2 * s + h) ^ T::swz_k(krow);
+                const u16x8 kf = *reinterpret_cast<const u16x8*>(kt + krow * D + pc * 8);
+                sacc[j] = Mfma<DT>::run(kf, qf[s], sacc[j]);
+            }
+        }
+        // K-fragment reads run kLook MFMAs ahead of their use (LDS latency > one MFMA).
+        {
+            constexpr int kLook = 4;
+            __builtin_amdgcn_sched_group_barrier(0x100, kLook, 0);  // DS reads
+#pragma unroll
+            for (int i = 0; i < NCB * S - kLook; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, kLook, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        after_s();
+#pragma unroll
+        for (int j = 0; j < NCB; ++j) {
+            const int cb = cb0 + j;
+            if (partial) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int key = base + 32 * cb + 8 * (i / 4) + 4 * h + (i % 4);
+                    if (key >= L) sacc[j][i] = -INFINITY;
+                }
+            }
+            float tmax = sacc[j][0];
+#pragma unroll
+            for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, sacc[j][i]);
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+            if (__any(tmax > m_run + lazy)) {
+                const float m_new = fmaxf(m_run, tmax);
+                const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
+                m_run = m_new;
+                neg_m = -m_new * scale_log2;
+                l_run *= alpha;
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) oacc[nb][i] *= alpha;
+            }
+            uint32_t pp[8];
+#pragma unroll
+            for (int i = 0; i < 16; i += 2) {
+                const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j][i], scale_log2, neg_m));
+                const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[j][i + 1], scale_log2, neg_m));
+                pp[i / 2] = Mfma<DT>::pack2(p0, p1);
+                l_run = Mfma<DT>::sum2(pp[i / 2], l_run);
+            }
+            // O^T += V^T P^T over the two 16-key k-steps of this 32-key half. The V^T
+            // fragment (channel 32nb + l%32, 8 keys) comes from two transpose reads: source
+            // lane r of each 16-lane group points at key 32cb+16kk+8t+4h+r/4, channels
+            // 32nb + 16*gsub + 4*(r%4) .. +3.
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                const u16x8 pf = __builtin_bit_cast(u16x8, u32x4{pp[4 * kk], pp[4 * kk + 1], pp[4 * kk + 2],
+                                                                pp[4 * kk + 3]});
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) {
+                    s16x4 part[2];
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+                        const int vrow = 32 * cb + 16 * kk + 8 * t + 4 * h + src / 4;
+                        const int d = 32 * nb + 16 * gsub + 4 * (src % 4);
+                        const int pc = (d / 8) ^ T::swz_v(vrow);
+                        const uint16_t* a = vt + vrow * D + pc * 8 + (d % 8);
+                        part[t] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                            (__attribute__((address_space(3))) s16x4*)(a));
+                    }
+                    const u16x8 af = __builtin_bit_cast(
+                        u16x8, u32x4{__builtin_bit_cast(u32x2, part[0])[0], __builtin_bit_cast(u32x2, part[0])[1],
+                                     __builtin_bit_cast(u32x2, part[1])[0], __builtin_bit_cast(u32x2, part[1])[1]});
+                    oacc[nb] = Mfma<DT>::run(af, pf, oacc[nb]);
+                }
+            }
+        }
+    };
     __syncthreads();
-    if (ntiles > 0) load_tile_lds<D>(ks[0], vs[0], kh, vh, prow[0], wave, lane);
+    if (ntiles > 0) load_tile_lds<D, 4>(ks[0], vs[0], kh, vh, prow[0], wave, lane);
     __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0): this wave's tile-0 loads have landed
     __syncthreads();
-    auto step = [&](auto bufc, int tile) {
+    auto step = [&](auto bufc, int tile) __attribute__((always_inline)) {
         constexpr int buf = decltype(bufc)::value;
         const bool more = tile + 1 < ntiles;
-        int ahead = 0;
+        // Row of tile t+3: a k_index value loaded into pidx (indexed) or the cluster cursor.
+        const int p3 = stream_pos((tile + 3) * kKTile + prow_entry);
         if constexpr (kIndexed) {
-            if (prow_owner && tile + 2 < ntiles) ahead = stream_row((tile + 2) * kKTile + prow_entry);
+            if (prow_owner) dma4(kidx + min(p3, oi_rows - 1), lds_addr(&pidx[buf][16 * wave]));
         }
-        if (more) load_tile_lds<D>(ks[buf ^ 1], vs[buf ^ 1], kh, vh, prow[buf ^ 1], wave, lane);
+        // Waves with rows only ever load as one of four loaders (the other counts mean idle
+        // waves carry the loads).
+        auto shared_load = [&]() __attribute__((always_inline)) {
+            if (more && loaders == 4) load_tile_lds<D, 4>(ks[buf ^ 1], vs[buf ^ 1], kh, vh, prow[buf ^ 1], wave, lane);
+        };
         if (wave_active) {
-            const int base = tile * kKTile;
-            const bool partial = base + kKTile > L;
-            const uint16_t* kt = ks[buf];
-            const uint16_t* vt = vs[buf];
-            // S^T for both 32-key halves first, so the softmax of one half overlaps MFMAs.
-            f32x16 sacc[2] = {f32x16{}, f32x16{}};
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-                const int krow = 32 * cb + arow;
-#pragma unroll
-                for (int s = 0; s < S; ++s) {
-                    const int pc = (2 * s + h) ^ T::swz_k(krow);
-                    const u16x8 kf = *reinterpret_cast<const u16x8*>(kt + krow * D + pc * 8);
-                    sacc[cb] = Mfma<DT>::run(kf, qf[s], sacc[cb]);
-                }
-            }
-            // K-fragment reads run kLook MFMAs ahead of their use (LDS latency > one MFMA).
-            {
-                constexpr int kLook = 4;
-                __builtin_amdgcn_sched_group_barrier(0x100, kLook, 0);  // DS reads
-#pragma unroll
-                for (int i = 0; i < 2 * S - kLook; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                }
-                __builtin_amdgcn_sched_group_barrier(0x008, kLook, 0);
-            }
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-                if (partial) {
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        const int key = base + 32 * cb + 8 * (i / 4) + 4 * h + (i % 4);
-                        if (key >= L) sacc[cb][i] = -INFINITY;
-                    }
-                }
-                float tmax = sacc[cb][0];
-#pragma unroll
-                for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, sacc[cb][i]);
-                tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
-                if (__any(tmax > m_run + lazy)) {
-                    const float m_new = fmaxf(m_run, tmax);
-                    const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
-                    m_run = m_new;
-                    neg_m = -m_new * scale_log2;
-                    l_run *= alpha;
-#pragma unroll
-                    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-                        for (int i = 0; i < 16; ++i) oacc[nb][i] *= alpha;
-                }
-                uint32_t pp[8];
-#pragma unroll
-                for (int i = 0; i < 16; i += 2) {
-                    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[cb][i], scale_log2, neg_m));
-                    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[cb][i + 1], scale_log2, neg_m));
-                    pp[i / 2] = Mfma<DT>::pack2(p0, p1);
-                    l_run = Mfma<DT>::sum2(pp[i / 2], l_run);
-                }
-                // O^T += V^T P^T over the two 16-key k-steps of this 32-key half. The V^T
-                // fragment (channel 32nb + l%32, 8 keys) comes from two transpose reads: source
-                // lane r of each 16-lane group points at key 32cb+16kk+8t+4h+r/4, channels
-                // 32nb + 16*gsub + 4*(r%4) .. +3.
-#pragma unroll
-                for (int kk = 0; kk < 2; ++kk) {
-                    const u16x8 pf = __builtin_bit_cast(u16x8, u32x4{pp[4 * kk], pp[4 * kk + 1], pp[4 * kk + 2],
-                                                                    pp[4 * kk + 3]});
-#pragma unroll
-                    for (int nb = 0; nb < NB; ++nb) {
-                        s16x4 part[2];
-#pragma unroll
-                        for (int t = 0; t < 2; ++t) {
-                            const int vrow = 32 * cb + 16 * kk + 8 * t + 4 * h + src / 4;
-                            const int d = 32 * nb + 16 * gsub + 4 * (src % 4);
-                            const int pc = (d / 8) ^ T::swz_v(vrow);
-                            const uint16_t* a = vt + vrow * D + pc * 8 + (d % 8);
-                            part[t] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                                (__attribute__((address_space(3))) s16x4*)(a));
-                        }
-                        const u16x8 af = __builtin_bit_cast(
-                            u16x8, u32x4{__builtin_bit_cast(u32x2, part[0])[0], __builtin_bit_cast(u32x2, part[0])[1],
-                                         __builtin_bit_cast(u32x2, part[1])[0], __builtin_bit_cast(u32x2, part[1])[1]});
-                        oacc[nb] = Mfma<DT>::run(af, pf, oacc[nb]);
-                    }
-                }
-            }
+            if constexpr (kSplit)
+                compute(std::integral_constant<int, 1>{}, hb, ks[buf], vs[buf], tile * kKTile, shared_load);
+            else
+                compute(std::integral_constant<int, 2>{}, 0, ks[buf], vs[buf], tile * kKTile, shared_load);
+        } else if (more && loader_rank >= 0) {
+            if (loaders == 4) load_tile_lds<D, 4>(ks[buf ^ 1], vs[buf ^ 1], kh, vh, prow[buf ^ 1], wave, lane);
+            else if (loaders == 2) load_tile_lds<D, 2>(ks[buf ^ 1], vs[buf ^ 1], kh, vh, prow[buf ^ 1], loader_rank, lane);
+            else load_tile_lds<D, 1>(ks[buf ^ 1], vs[buf ^ 1], kh, vh, prow[buf ^ 1], loader_rank, lane);
         }
-        if constexpr (kIndexed) {
-            if (prow_owner && tile + 2 < ntiles) prow[buf][prow_entry] = ahead;
-        } else {
-            if (more && tid < kKTile) prow[buf][tid] = stream_row((tile + 2) * kKTile + tid);
-        }
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of the next tile have landed
-        __syncthreads();
+        if (prow_owner) prow[buf][prow_entry] = row2;
+        // This wave's tile t+1 loads and its index load have landed.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if constexpr (kIndexed) row2 = physical(p3, pidx[buf][prow_entry]);
+        else row2 = p3;
+        // The barrier publishes LDS only (prow, the tile t+1 loads, waited for above), so it
+        // carries LDS-scoped fences instead of __syncthreads' full ones.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     };
     for (int tile = 0; tile < ntiles; tile += 2) {
         step(std::integral_constant<int, 0>{}, tile);
         if (tile + 1 < ntiles) step(std::integral_constant<int, 1>{}, tile + 1);
+    }
+    if constexpr (kSplit) {
+        // Merge the pair's states: the second-half wave (hb = 1) leaves m, l and O in the tile
+        // LDS (free after the loop's last barrier), the first-half wave rescales both to the
+        // larger maximum and adds. Lane l of both waves holds the same query rows.
+        float* xch = reinterpret_cast<float*>(&ks[0][0]) + (rb * kWave + lane) * (NB * 16 + 2);
+        if (hb == 1 && wave_active) {
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) xch[nb * 16 + i] = oacc[nb][i];
+            xch[NB * 16] = m_run;
+            xch[NB * 16 + 1] = l_run;
+        }
+        __syncthreads();
+        if (hb == 1) return;
+        if (wave_active) {
+            const float m1 = xch[NB * 16], l1 = xch[NB * 16 + 1];
+            const float m = fmaxf(m_run, m1);
+            // A half without keys has m = -inf (and l = 0, O = 0); both empty leaves O at 0.
+            const float a0 = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_run - m) * scale_log2);
+            const float a1 = m1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m1 - m) * scale_log2);
+            l_run = l_run * a0 + l1 * a1;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) oacc[nb][i] = oacc[nb][i] * a0 + xch[nb * 16 + i] * a1;
+        }
     }
     if (!qvalid) return;
     const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
@@ -677,6 +794,35 @@ PECO_API size_t peco_sparse_attention_workspace_size(int bh, int sq, int sk, int
 namespace peco {
 namespace {
 
+// Side stream of the short-item launch, with its fork and join events: one set per host
+// thread and device (created on first use, kept until the process ends), so that concurrent
+// callers never share an event. Default priority, non-blocking.
+struct SideStream {
+    hipStream_t stream = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+    hipError_t status = hipErrorNotInitialized;
+};
+
+SideStream& side_stream() {
+    constexpr int kMaxDevices = 64;
+    thread_local SideStream sets[kMaxDevices];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    static SideStream failed;
+    if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        failed.status = e != hipSuccess ? e : hipErrorInvalidDevice;
+        return failed;
+    }
+    SideStream& ss = sets[dev];
+    if (ss.status == hipErrorNotInitialized) {
+        e = hipStreamCreateWithFlags(&ss.stream, hipStreamNonBlocking);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&ss.join, hipEventDisableTiming);
+        ss.status = e;
+    }
+    return ss;
+}
+
 // Shared launcher: k_index (nullable) selects the indexed-input kernel (inputs in original
 // token order, read through out_index for Q and k_index for K/V).
 int launch_sparse_attention(const void* q, const void* k, const void* v, const uint8_t* selected,
@@ -692,7 +838,7 @@ int launch_sparse_attention(const void* q, const void* k, const void* v, const u
     if (sq == 0) return kOk;
     if (workspace_ints < peco_sparse_attention_workspace_size(bh, sq, sk, cq, ck)) return kWorkspaceTooSmall;
     const size_t lds_build = build_lds_bytes(cq, ck);
-    const size_t lds_attn = sizeof(int) * (2 * static_cast<size_t>(ck) + 1);
+    const size_t lds_attn = sizeof(int) * 2 * (static_cast<size_t>(ck) + 1 + kGallop);
     if (lds_build > 60 * 1024 || lds_attn > 24 * 1024) return kUnsupportedShape;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (kept_keys)
@@ -708,9 +854,24 @@ int launch_sparse_attention(const void* q, const void* k, const void* v, const u
     const auto* kp = static_cast<const uint16_t*>(k);
     const auto* vp = static_cast<const uint16_t*>(v);
     auto* op = static_cast<uint16_t*>(output);
+    // Two launches over the same work list, each skipping the other's items: items of more
+    // than kSplitRows rows on the caller's stream, the short ones (paired waves) on a side
+    // stream forked from and joined back into it, so that their workgroups fill the slots the
+    // long items leave instead of running after them.
+    SideStream& side = side_stream();
+    if (side.status != hipSuccess) return side.status;
+    hipError_t e = hipEventRecord(side.fork, s);
+    if (e == hipSuccess) e = hipStreamWaitEvent(side.stream, side.fork, 0);
+    if (e != hipSuccess) return e;
 #define PECO_ATTN(DT_, D_, IX_)                                                                                    \
-    hipLaunchKernelGGL((sparse_attention_kernel<DT_, D_, IX_>), grid, dim3(256), lds_attn, s, qp, kp, vp, selected, \
-                       workspace, op, out_index, out_index_rows, k_index, bh, sq, sk, cq, ck, scale_log2)
+    do {                                                                                                           \
+        hipLaunchKernelGGL((sparse_attention_kernel<DT_, D_, IX_, true>), grid, dim3(256), lds_attn, side.stream, qp, \
+                           kp, vp, selected, workspace, op, out_index, out_index_rows, k_index, bh, sq, sk, cq, ck, \
+                           scale_log2);                                                                            \
+        hipLaunchKernelGGL((sparse_attention_kernel<DT_, D_, IX_, false>), grid, dim3(256), lds_attn, s, qp, kp, vp, \
+                           selected, workspace, op, out_index, out_index_rows, k_index, bh, sq, sk, cq, ck,        \
+                           scale_log2);                                                                            \
+    } while (0)
 #define PECO_ATTN_D(DT_, IX_)                                                                                      \
     do {                                                                                                           \
         if (d == 128) PECO_ATTN(DT_, 128, IX_);                                                                    \
@@ -725,7 +886,11 @@ int launch_sparse_attention(const void* q, const void* k, const void* v, const u
     }
 #undef PECO_ATTN_D
 #undef PECO_ATTN
-    return hipGetLastError();
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    e = hipEventRecord(side.join, side.stream);
+    if (e == hipSuccess) e = hipStreamWaitEvent(s, side.join, 0);
+    return e;
 }
 
 }  // namespace
