@@ -35,7 +35,7 @@ namespace {
 constexpr int kQTile = 128;   // query rows per item (4 waves x 32)
 constexpr int kKTile = 64;    // keys per LDS tile
 constexpr int kSortCap = 2048;
-constexpr int kSplitRows = 64;  // items up to this many rows run in the paired-wave launch
+constexpr int kSplitRows = 64;  // items up to this many rows pair their waves
 constexpr int kGallop = 8;      // key-stream segments a row lookup examines at once
 
 struct WorkLayout {
@@ -435,7 +435,7 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 // kIndexed: the inputs are in their original token order. Query row j < oi_rows of a head is
 // read from row out_index[j] (the same permutation that scatters the output) and key/value
 // stream row p < oi_rows from row k_index[p]; rows past oi_rows (text) keep their position.
-template <int DT, int D, bool kIndexed, bool kSplit>
+template <int DT, int D, bool kIndexed>
 __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint8_t* __restrict__ selected, const int32_t* __restrict__ ws, uint16_t* __restrict__ out,
@@ -463,7 +463,6 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     if (slot >= W.counts[bh]) return;
     const int32_t* item = W.items + (static_cast<int64_t>(bh) * W.cap + slot) * 3;
     const int q_start = item[0], qc = item[1], q_rows = item[2];
-    if ((q_rows <= kSplitRows) != kSplit) return;  // the other launch's item
     const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave, h = lane / 32;
 
     const uint8_t* sel = selected + (static_cast<int64_t>(bh) * cq + qc) * ck;
@@ -549,20 +548,21 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     }
     int row2 = stream_row(2 * kKTile + prow_entry);  // this lane's row of tile t+2
 
-    // kSplit (items of at most kSplitRows rows) pairs the waves: wave w takes 32-row block
-    // w & 1 and, of every tile, only the 32-key half w >> 1, so a short item's tiles cost half
-    // the time; each pair merges its two partial softmax states after the last tile. Longer
-    // items give each wave its own row block and both halves of every tile.
-    const int rb = kSplit ? (wave & 1) : wave;  // this wave's 32-row block
-    const int hb = kSplit ? (wave >> 1) : 0;    // first 32-key half this wave processes
+    // Items of at most kSplitRows rows pair the waves: wave w takes 32-row block w & 1 and, of
+    // every tile, only the 32-key half w >> 1, so a short item's tiles cost about half the
+    // time; each pair merges its two partial softmax states after the last tile. Longer items
+    // give each wave its own row block and both halves of every tile.
+    const bool split = q_rows <= kSplitRows;
+    const int rb = split ? (wave & 1) : wave;  // this wave's 32-row block
+    const int hb = split ? (wave >> 1) : 0;    // first 32-key half this wave processes
     // Waves without query rows issue every tile load, so that waiting for the load path to
     // accept them never delays a wave with MFMA work; with no such wave all four share.
     const int row_blocks = static_cast<int>(ceil_div(q_rows, 32));
-    const int idle = kSplit ? 4 - 2 * row_blocks : 4 - row_blocks;   // waves 4-idle .. 3 (or 1, 3)
+    const int idle = split ? 4 - 2 * row_blocks : 4 - row_blocks;   // waves 4-idle .. 3 (or 1, 3)
     const int loaders = idle >= 2 ? 2 : (idle == 1 ? 1 : 4);
     int loader_rank;
     if (loaders == 4) loader_rank = wave;
-    else if constexpr (kSplit) loader_rank = (wave & 1) ? wave >> 1 : -1;   // idle waves 1 and 3
+    else if (split) loader_rank = (wave & 1) ? wave >> 1 : -1;   // idle waves 1 and 3
     else loader_rank = wave >= 4 - loaders ? wave - (4 - loaders) : -1;
     // Q^T operand: lane holds query row (32*rb + l%32), channels 16s + 8h .. +7.
     const int qrow = rb * 32 + (lane % 32);
@@ -703,10 +703,10 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
             if (more && loaders == 4) load_tile_lds<D, 4>(ks[buf ^ 1], vs[buf ^ 1], kh, vh, prow[buf ^ 1], wave, lane);
         };
         if (wave_active) {
-            if constexpr (kSplit)
-                compute(std::integral_constant<int, 1>{}, hb, ks[buf], vs[buf], tile * kKTile, shared_load);
-            else
-                compute(std::integral_constant<int, 2>{}, 0, ks[buf], vs[buf], tile * kKTile, shared_load);
+            // Key half hb (with the next tile's loads issued behind its S^T MFMAs), then, for
+            // unpaired waves, the other half.
+            compute(std::integral_constant<int, 1>{}, hb, ks[buf], vs[buf], tile * kKTile, shared_load);
+            if (!split) compute(std::integral_constant<int, 1>{}, 1, ks[buf], vs[buf], tile * kKTile, [] {});
         } else if (more && loader_rank >= 0) {
             if (loaders == 4) load_tile_lds<D, 4>(ks[buf ^ 1], vs[buf ^ 1], kh, vh, prow[buf ^ 1], wave, lane);
             else if (loaders == 2) load_tile_lds<D, 2>(ks[buf ^ 1], vs[buf ^ 1], kh, vh, prow[buf ^ 1], loader_rank, lane);
@@ -727,7 +727,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
         step(std::integral_constant<int, 0>{}, tile);
         if (tile + 1 < ntiles) step(std::integral_constant<int, 1>{}, tile + 1);
     }
-    if constexpr (kSplit) {
+    if (split) {
         // Merge the pair's states: the second-half wave (hb = 1) leaves m, l and O in the tile
         // LDS (free after the loop's last barrier), the first-half wave rescales both to the
         // larger maximum and adds. Lane l of both waves holds the same query rows.
@@ -794,35 +794,6 @@ PECO_API size_t peco_sparse_attention_workspace_size(int bh, int sq, int sk, int
 namespace peco {
 namespace {
 
-// Side stream of the short-item launch, with its fork and join events: one set per host
-// thread and device (created on first use, kept until the process ends), so that concurrent
-// callers never share an event. Default priority, non-blocking.
-struct SideStream {
-    hipStream_t stream = nullptr;
-    hipEvent_t fork = nullptr, join = nullptr;
-    hipError_t status = hipErrorNotInitialized;
-};
-
-SideStream& side_stream() {
-    constexpr int kMaxDevices = 64;
-    thread_local SideStream sets[kMaxDevices];
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    static SideStream failed;
-    if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
-        failed.status = e != hipSuccess ? e : hipErrorInvalidDevice;
-        return failed;
-    }
-    SideStream& ss = sets[dev];
-    if (ss.status == hipErrorNotInitialized) {
-        e = hipStreamCreateWithFlags(&ss.stream, hipStreamNonBlocking);
-        if (e == hipSuccess) e = hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming);
-        if (e == hipSuccess) e = hipEventCreateWithFlags(&ss.join, hipEventDisableTiming);
-        ss.status = e;
-    }
-    return ss;
-}
-
 // Shared launcher: k_index (nullable) selects the indexed-input kernel (inputs in original
 // token order, read through out_index for Q and k_index for K/V).
 int launch_sparse_attention(const void* q, const void* k, const void* v, const uint8_t* selected,
@@ -854,24 +825,9 @@ int launch_sparse_attention(const void* q, const void* k, const void* v, const u
     const auto* kp = static_cast<const uint16_t*>(k);
     const auto* vp = static_cast<const uint16_t*>(v);
     auto* op = static_cast<uint16_t*>(output);
-    // Two launches over the same work list, each skipping the other's items: items of more
-    // than kSplitRows rows on the caller's stream, the short ones (paired waves) on a side
-    // stream forked from and joined back into it, so that their workgroups fill the slots the
-    // long items leave instead of running after them.
-    SideStream& side = side_stream();
-    if (side.status != hipSuccess) return side.status;
-    hipError_t e = hipEventRecord(side.fork, s);
-    if (e == hipSuccess) e = hipStreamWaitEvent(side.stream, side.fork, 0);
-    if (e != hipSuccess) return e;
 #define PECO_ATTN(DT_, D_, IX_)                                                                                    \
-    do {                                                                                                           \
-        hipLaunchKernelGGL((sparse_attention_kernel<DT_, D_, IX_, true>), grid, dim3(256), lds_attn, side.stream, qp, \
-                           kp, vp, selected, workspace, op, out_index, out_index_rows, k_index, bh, sq, sk, cq, ck, \
-                           scale_log2);                                                                            \
-        hipLaunchKernelGGL((sparse_attention_kernel<DT_, D_, IX_, false>), grid, dim3(256), lds_attn, s, qp, kp, vp, \
-                           selected, workspace, op, out_index, out_index_rows, k_index, bh, sq, sk, cq, ck,        \
-                           scale_log2);                                                                            \
-    } while (0)
+    hipLaunchKernelGGL((sparse_attention_kernel<DT_, D_, IX_>), grid, dim3(256), lds_attn, s, qp, kp, vp, selected, \
+                       workspace, op, out_index, out_index_rows, k_index, bh, sq, sk, cq, ck, scale_log2)
 #define PECO_ATTN_D(DT_, IX_)                                                                                      \
     do {                                                                                                           \
         if (d == 128) PECO_ATTN(DT_, 128, IX_);                                                                    \
@@ -886,11 +842,7 @@ int launch_sparse_attention(const void* q, const void* k, const void* v, const u
     }
 #undef PECO_ATTN_D
 #undef PECO_ATTN
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    e = hipEventRecord(side.join, side.stream);
-    if (e == hipSuccess) e = hipStreamWaitEvent(s, side.join, 0);
-    return e;
+    return hipGetLastError();
 }
 
 }  // namespace
