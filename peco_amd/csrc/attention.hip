@@ -36,7 +36,6 @@ constexpr int kQTile = 128;   // query rows per item (4 waves x 32)
 constexpr int kKTile = 64;    // keys per LDS tile
 constexpr int kSortCap = 2048;
 constexpr int kSplitRows = 64;  // items up to this many rows pair their waves
-constexpr int kGallop = 8;      // key-stream segments a row lookup examines at once
 
 struct WorkLayout {
     int32_t* counts;   // [bh]
@@ -454,8 +453,8 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     extern __shared__ int dyn[];
     // Key stream of this query cluster: the kept, non-empty key clusters in order. Segment i
     // is {first physical row - stream offset, stream offset} of the i-th of them, followed by
-    // kGallop + 1 sentinels whose offset no stream row reaches.
-    int2* kseg = reinterpret_cast<int2*>(dyn);  // [ck + 1 + kGallop]
+    // a sentinel whose offset no stream row reaches.
+    int2* kseg = reinterpret_cast<int2*>(dyn);  // [ck + 1]
 
     const int bh = blockIdx.x % bhn;
     const int slot = blockIdx.x / bhn;
@@ -489,40 +488,24 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
                 run += e - a;
             }
         }
-        if (tid <= kGallop) kseg[nk + tid] = int2{0, 0x7fffffff};
+        if (tid == 0) kseg[nk] = int2{0, 0x7fffffff};
     }
     __syncthreads();
     const int ntiles = static_cast<int>(ceil_div(L, kKTile));
     // Physical row of stream row r (r < L). Every lane asks for increasing rows (its row of
-    // every tile), so a forward-only cursor over the segments suffices. The next kGallop
-    // segment offsets are read at once (independent LDS reads, no loop) and the ones <= r
-    // counted; only a jump over more segments than that continues one at a time.
+    // every tile), so a forward-only cursor over the segments suffices.
     int cur = 0;
     auto row_of = [&](int r) {
-        int2 seg[kGallop + 1];
-#pragma unroll
-        for (int j = 0; j <= kGallop; ++j) seg[j] = kseg[cur + j];
-        int adv = 0;
-#pragma unroll
-        for (int j = 1; j <= kGallop; ++j) adv += seg[j].y <= r ? 1 : 0;
-        int delta = seg[0].x;
-#pragma unroll
-        for (int j = 1; j <= kGallop; ++j) delta = adv >= j ? seg[j].x : delta;
-        cur += adv;
-        if (adv == kGallop) {
-            while (kseg[cur + 1].y <= r) ++cur;
-            delta = kseg[cur].x;
-        }
-        return r + delta;
+        while (kseg[cur + 1].y <= r) ++cur;
+        return r + kseg[cur].x;
     };
     // Tile rows move through a pipeline. Lane l of wave w follows tile row 16*w + l%16 (lanes
-    // 0..15 own it, the others shadow it). During tile t it
-    //   - asks for the physical row of tile t+3 (indexed inputs: its k_index value is loaded
-    //     straight into pidx),
-    //   - issues the direct-to-LDS loads of tile t+1 (rows in prow, written a tile earlier)
-    //     right after its S^T MFMAs,
-    // and at the end it publishes its tile t+2 row in prow. Every load of the loop goes
-    // straight to LDS (no register is written behind the compiler's back), so the loop
+    // 0..15 own it, the others shadow it). During tile t it issues the direct-to-LDS loads of
+    // tile t+1 (rows in prow, written a tile earlier) right after its S^T MFMAs; at the end,
+    // off the MFMAs' path, it looks up its tile t+2 row and publishes it in prow. Indexed
+    // inputs look two tiles further: the k_index value of the tile t+3 row is loaded straight
+    // into pidx at the end of tile t and used at the end of tile t+1. Every load of the loop
+    // goes straight to LDS (no register is written behind the compiler's back), so the loop
     // waits for them explicitly.
     const int64_t head = static_cast<int64_t>(bh);
     const int32_t* kidx = kIndexed ? k_index + head * oi_rows : nullptr;
@@ -542,11 +525,15 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
         if constexpr (kIndexed) return physical(p, kidx[min(p, oi_rows - 1)]);
         else return p;
     };
+    int p2 = 0;  // indexed: this lane's stream position in tile t+2 (its k_index value is in pidx)
     if (prow_owner) {
         prow[0][prow_entry] = stream_row(prow_entry);
         prow[1][prow_entry] = stream_row(kKTile + prow_entry);
     }
-    int row2 = stream_row(2 * kKTile + prow_entry);  // this lane's row of tile t+2
+    if constexpr (kIndexed) {
+        p2 = stream_pos(2 * kKTile + prow_entry);
+        if (prow_owner) pidx[1][prow_entry] = kidx[min(p2, oi_rows - 1)];
+    }
 
     // Items of at most kSplitRows rows pair the waves: wave w takes 32-row block w & 1 and, of
     // every tile, only the 32-key half w >> 1, so a short item's tiles cost about half the
@@ -692,11 +679,6 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     auto step = [&](auto bufc, int tile) __attribute__((always_inline)) {
         constexpr int buf = decltype(bufc)::value;
         const bool more = tile + 1 < ntiles;
-        // Row of tile t+3: a k_index value loaded into pidx (indexed) or the cluster cursor.
-        const int p3 = stream_pos((tile + 3) * kKTile + prow_entry);
-        if constexpr (kIndexed) {
-            if (prow_owner) dma4(kidx + min(p3, oi_rows - 1), lds_addr(&pidx[buf][16 * wave]));
-        }
         // Waves with rows only ever load as one of four loaders (the other counts mean idle
         // waves carry the loads).
         auto shared_load = [&]() __attribute__((always_inline)) {
@@ -712,11 +694,18 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
             else if (loaders == 2) load_tile_lds<D, 2>(ks[buf ^ 1], vs[buf ^ 1], kh, vh, prow[buf ^ 1], loader_rank, lane);
             else load_tile_lds<D, 1>(ks[buf ^ 1], vs[buf ^ 1], kh, vh, prow[buf ^ 1], loader_rank, lane);
         }
-        if (prow_owner) prow[buf][prow_entry] = row2;
-        // This wave's tile t+1 loads and its index load have landed.
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        if constexpr (kIndexed) row2 = physical(p3, pidx[buf][prow_entry]);
-        else row2 = p3;
+        if constexpr (kIndexed) {
+            const int p3 = stream_pos((tile + 3) * kKTile + prow_entry);
+            if (prow_owner) dma4(kidx + min(p3, oi_rows - 1), lds_addr(&pidx[buf][16 * wave]));
+            // Everything but that index load has landed: this wave's tile t+1 loads and the
+            // index loaded a tile ago (pidx[buf ^ 1]).
+            asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
+            if (prow_owner) prow[buf][prow_entry] = physical(p2, pidx[buf ^ 1][prow_entry]);
+            p2 = p3;
+        } else {
+            if (prow_owner) prow[buf][prow_entry] = stream_pos((tile + 2) * kKTile + prow_entry);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's tile t+1 loads
+        }
         // The barrier publishes LDS only (prow, the tile t+1 loads, waited for above), so it
         // carries LDS-scoped fences instead of __syncthreads' full ones.
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
@@ -727,6 +716,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
         step(std::integral_constant<int, 0>{}, tile);
         if (tile + 1 < ntiles) step(std::integral_constant<int, 1>{}, tile + 1);
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last index load
     if (split) {
         // Merge the pair's states: the second-half wave (hb = 1) leaves m, l and O in the tile
         // LDS (free after the loop's last barrier), the first-half wave rescales both to the
@@ -809,7 +799,7 @@ int launch_sparse_attention(const void* q, const void* k, const void* v, const u
     if (sq == 0) return kOk;
     if (workspace_ints < peco_sparse_attention_workspace_size(bh, sq, sk, cq, ck)) return kWorkspaceTooSmall;
     const size_t lds_build = build_lds_bytes(cq, ck);
-    const size_t lds_attn = sizeof(int) * 2 * (static_cast<size_t>(ck) + 1 + kGallop);
+    const size_t lds_attn = sizeof(int) * 2 * (static_cast<size_t>(ck) + 1);
     if (lds_build > 60 * 1024 || lds_attn > 24 * 1024) return kUnsupportedShape;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (kept_keys)
