@@ -52,7 +52,7 @@ struct KmProblem {
     float* sums;            // nullable [batch, K, D]: per-cluster sums of the last update
     int batch, tokens, clusters;
     int assign_begin;       // first linear assign block of this problem
-    int assign_blocks;      // batch * ceil(tokens / 256)
+    int assign_blocks;      // batch * ceil(tokens / kAssignTile)
     int update_begin;       // first linear prep block (batch * K blocks)
     int scan_begin;         // first linear update workgroup (batch * ceil(K / 8))
     int scan_blocks;
@@ -63,7 +63,9 @@ struct KmProblem {
 };
 
 constexpr int kMaxKm = 2;
-constexpr int kAssignTile = 256;  // tokens per assign workgroup (4 waves x 64 tokens)
+constexpr int kAssignWaves = 4;                    // wavefronts per assign workgroup
+constexpr int kAssignThreads = kAssignWaves * 64;
+constexpr int kAssignTile = kAssignWaves * 64;      // tokens per assign workgroup (64 per wave)
 
 struct KmArgs {
     KmProblem p[kMaxKm];
@@ -199,8 +201,9 @@ __device__ __forceinline__ void split_x8(const XChunk<DT>& r, bool valid, u16x8&
     sq += valid ? part : 0.0f;
 }
 
-// Assign: one workgroup = 256 tokens of one (problem, batch); wave w owns tokens
-// [64w, 64w+64) as two 32-token MFMA column blocks. Centres stream through LDS in blocks of
+// Assign: one workgroup = kAssignTile tokens of one (problem, batch); wave w owns tokens
+// [64w, 64w+64) as two 32-token MFMA column blocks (two-wave workgroups, four per CU,
+// measured no faster). Centres stream through LDS in blocks of
 // 32 (split-bf16 hi/lo rows + canonical norms), double-buffered with a register prefetch.
 // MFMA 32x32x16: A = centres (32 rows x 16 channels), B = tokens (16 channels x 32 tokens);
 // lane l holds token l%32 of each column block and centres 8*(i/4)+4*(l/32)+i%4.
@@ -215,7 +218,7 @@ template <int D> struct AssignTiles {
     static constexpr int kRow = D + 8;                 // padded LDS row (16-bit elements)
     static constexpr int kElems = 32 * kRow;
     static constexpr int kChunks = D / 8;              // 16-byte chunks per row
-    static constexpr int kLoads = 32 * kChunks / 256;  // 16-byte loads per thread per array
+    static constexpr int kLoads = 32 * kChunks / kAssignThreads;  // 16-byte loads per thread per array
 };
 
 template <int D> struct CentreRegs {
@@ -229,7 +232,7 @@ __device__ __forceinline__ void load_centres(CentreRegs<D>& R, const uint16_t* h
     using T = AssignTiles<D>;
 #pragma unroll
     for (int i = 0; i < T::kLoads; ++i) {
-        const int id = i * 256 + tid;
+        const int id = i * kAssignThreads + tid;
         const int row = min(cb + id / T::kChunks, K - 1);  // rows past K are never selected
         const int64_t e = static_cast<int64_t>(row) * D + (id % T::kChunks) * 8;
         R.hi[i] = *reinterpret_cast<const u32x4*>(hi_base + e);
@@ -243,7 +246,7 @@ __device__ __forceinline__ void store_centres(const CentreRegs<D>& R, uint16_t* 
     using T = AssignTiles<D>;
 #pragma unroll
     for (int i = 0; i < T::kLoads; ++i) {
-        const int id = i * 256 + tid;
+        const int id = i * kAssignThreads + tid;
         const int off = (id / T::kChunks) * T::kRow + (id % T::kChunks) * 8;
         *reinterpret_cast<u32x4*>(hi + off) = R.hi[i];
         *reinterpret_cast<u32x4*>(lo + off) = R.lo[i];
@@ -288,14 +291,14 @@ __device__ __forceinline__ float canonical_dot(const void* x, int64_t xrow, cons
 }
 
 template <int DT, int D>
-__global__ __launch_bounds__(256, 2) void km_assign_kernel(KmArgs a, KmIter it) {
+__global__ __launch_bounds__(kAssignThreads, 2) void km_assign_kernel(KmArgs a, KmIter it) {
     using T = AssignTiles<D>;
     constexpr int S = D / 16;                 // MFMA k-steps over channels
     constexpr bool kSplitX = DT != kBF16;
     __shared__ uint16_t chi[2][T::kElems];
     __shared__ uint16_t clo[2][T::kElems];
     __shared__ float cn[2][32];
-    __shared__ float red[4];
+    __shared__ float red[kAssignWaves];
     const int p = km_problem(a, blockIdx.x, true);
     const KmProblem& P = a.p[p];
     const int local = blockIdx.x - P.assign_begin;
@@ -359,7 +362,9 @@ __global__ __launch_bounds__(256, 2) void km_assign_kernel(KmArgs a, KmIter it) 
     }
     store_centres<D>(regs, chi[0], clo[0], cn[0], tid);
     __syncthreads();
-    nmax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    nmax = red[0];
+#pragma unroll
+    for (int w = 1; w < kAssignWaves; ++w) nmax = fmaxf(nmax, red[w]);
 
     // Sorted kTop smallest screened values per token and lane half (t[0] <= t[1] <= ...). The centre index
     // j is packed into the low `ibits` mantissa bits, so min/med3 track value and index
@@ -846,7 +851,8 @@ template <int DT, int D>
 hipError_t run_fit(KmArgs& a, const KmIter* iters, int iterations, SortArgs sa, hipStream_t s) {
     hipLaunchKernelGGL((km_prep_kernel<D>), dim3(a.total_update_blocks), dim3(64), 0, s, a, iters[0]);
     for (int i = 0; i < iterations; ++i) {
-        hipLaunchKernelGGL((km_assign_kernel<DT, D>), dim3(a.total_assign_blocks), dim3(256), 0, s, a, iters[i]);
+        hipLaunchKernelGGL((km_assign_kernel<DT, D>), dim3(a.total_assign_blocks), dim3(kAssignThreads), 0, s, a,
+                           iters[i]);
         // The sort reads the histograms this iteration's assign filled. The fused sort leaves
         // them intact and clears the other set, which the next iteration's assign fills.
         for (int q = 0; q < a.num; ++q) {
@@ -1097,10 +1103,10 @@ PECO_API int peco_assign_tokens_to_centers(const float* x, const float* centers,
     it.src[0] = centers;
     if (dims == 128) {
         hipLaunchKernelGGL((km_prep_kernel<128>), dim3(a.total_update_blocks), dim3(64), 0, s, a, it);
-        hipLaunchKernelGGL((km_assign_kernel<kF32, 128>), dim3(a.total_assign_blocks), dim3(256), 0, s, a, it);
+        hipLaunchKernelGGL((km_assign_kernel<kF32, 128>), dim3(a.total_assign_blocks), dim3(kAssignThreads), 0, s, a, it);
     } else {
         hipLaunchKernelGGL((km_prep_kernel<64>), dim3(a.total_update_blocks), dim3(64), 0, s, a, it);
-        hipLaunchKernelGGL((km_assign_kernel<kF32, 64>), dim3(a.total_assign_blocks), dim3(256), 0, s, a, it);
+        hipLaunchKernelGGL((km_assign_kernel<kF32, 64>), dim3(a.total_assign_blocks), dim3(kAssignThreads), 0, s, a, it);
     }
     e = hipGetLastError();
     hipError_t f = hipFreeAsync(buf, s);

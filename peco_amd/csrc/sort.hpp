@@ -5,8 +5,8 @@
 
 namespace peco {
 
-// Tokens per sort tile: one tile is ranked by a single wavefront, 64 tokens per step. It
-// equals the k-means assign tile, so each tile histogram row has a single producer.
+// Tokens per sort tile: one tile is ranked by a single wavefront, 64 tokens per step. The
+// k-means assign kernel adds its labels to these histograms with atomics.
 constexpr int kSortTile = 256;
 constexpr int kMaxSortClusters = 16384;
 
