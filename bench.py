@@ -41,8 +41,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--stage-reps", type=int, default=10)
-    ap.add_argument("--profile-target", choices=("attention", "copy"), default=None,
-                    help="replay only the attention launch, or a plain device copy of --copy-mib MiB, --reps times "
+    ap.add_argument("--profile-target", choices=("attention", "kmeans", "pack", "copy"), default=None,
+                    help="replay only the attention launch, the Q+K k-means fit, the pack launch (fake-quant and "
+                         "gather; Base-Offset workloads) or a plain device copy of --copy-mib MiB, --reps times "
                          "(for rocprofv3 counter runs)")
     ap.add_argument("--reps", type=int, default=10)
     ap.add_argument("--copy-mib", type=int, default=1024)
@@ -212,11 +213,53 @@ def profile_target(args):
         print(f"copy {args.copy_mib} MiB x {args.reps}: reads {args.copy_mib * 1024} KiB and writes "
               f"{args.copy_mib * 1024} KiB per dispatch", flush=True)
         return
-    from peco_amd import workloads
+    from peco_amd import clustering_cuda, workloads
 
     wl = workloads.make_workload(args.workload, device=dev)
+    s = wl.shape
     layer = make_layer(wl)
+    n = s.video
     with torch.no_grad():
+        if args.profile_target == "kmeans":
+            # The layer's fused Q+K fit from the seeded centroids (stage 1).
+            problems = [clustering_cuda.KMeansProblem(wl.query[0, :, :n], wl.q_init),
+                        clustering_cuda.KMeansProblem(wl.key[0, :, :n], wl.k_init)]
+            clustering_cuda.kmeans_fit(problems, s.iterations)
+            torch.cuda.synchronize()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            for _ in range(args.reps):
+                clustering_cuda.kmeans_fit(problems, s.iterations)
+            end.record()
+            torch.cuda.synchronize()
+            t = start.elapsed_time(end) / args.reps
+            f1 = 2.0 * s.dims * n * (s.num_q_centroids + s.num_k_centroids) * s.heads * s.iterations
+            print(f"kmeans fit {t * 1e3:.1f} us, F1 {f1:.6g} FLOPs ({f1 / (t * 1e-3) / 1e12:.1f} TFLOP/s); "
+                  f"per iteration and launch: assign, sort, update", flush=True)
+            return
+        if args.profile_target == "pack":
+            # Stages 2+3: fake-quant Q/K against their centroids and gather Q/K/V into cluster order.
+            layer.q_centroids, layer.k_centroids = wl.q_init, wl.k_init
+            ql, kl, _, _ = layer._update_cluster_state(wl.query[:, :, :n], wl.key[:, :, :n])
+            q_idx, k_idx = layer._last_fit
+            pack_args = ([wl.query, wl.key, wl.value], [q_idx, k_idx, k_idx], [ql, kl, None],
+                         [layer.q_centroids, layer.k_centroids, None], [s.bits, s.bits, 0], n)
+            clustering_cuda.pack_clustered(*pack_args)
+            torch.cuda.synchronize()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            for _ in range(args.reps):
+                clustering_cuda.pack_clustered(*pack_args)
+            end.record()
+            torch.cuda.synchronize()
+            t = start.elapsed_time(end) / args.reps
+            # B2 + B3 of the pack: read x and write x-hat for Q, K (2D bytes each way per row, plus
+            # label and index) and V (gather only), text rows copied.
+            rows = s.heads * s.length
+            b = 3 * rows * 2 * s.dims * 2 + s.heads * n * (4 + 4) * 2 + s.heads * n * 4
+            print(f"pack launch {t * 1e3:.1f} us, algorithmic {b:.6g} bytes ({b / (t * 1e-3) / 1e9:.0f} GB/s)",
+                  flush=True)
+            return
         _, flops, attn_args = stage_breakdown(layer, wl, wl.query, wl.key, wl.value, wl.q_init, wl.k_init, 1)
         t = attention_kernel_time(attn_args, args.reps)
     print(f"attention launch {t * 1e3:.1f} us, {flops / (t * 1e-3) / 1e12:.1f} TFLOP/s, flops {flops:.6g}",

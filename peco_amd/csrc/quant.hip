@@ -89,10 +89,19 @@ __device__ __forceinline__ void base_offset_lane(const float (&x)[8], const floa
     const float span = hi - lo;
     const float raw = span / levels;
     const float scale = raw > 0.0f ? raw : 1.0f;
+    // code = rint(RN(shifted / scale)) with the division done once per row: qa = shifted * inv
+    // (inv = RN(1 / scale)) and Q = shifted / scale satisfy |qa - Q| <= Q * (2^-23 + 2^-48),
+    // and |RN(Q) - Q| <= Q * 2^-24 with Q <= levels, so rint(qa) == rint(RN(Q)) unless qa lies
+    // within levels * 1.8e-7 of a half-integer. There (tol = levels * 2^-21 with margin; the
+    // distance qa - rint(qa) is computed exactly) the correctly rounded division decides.
+    const float inv = 1.0f / scale;
+    const float tol = levels * 4.76837158203125e-7f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const float shifted = r[i] - lo;
-        float q = __builtin_rintf(shifted / scale);
+        const float qa = shifted * inv;
+        float q = __builtin_rintf(qa);
+        if (fabsf(qa - q) >= 0.5f - tol) q = __builtin_rintf(shifted / scale);
         q = q < 0.0f ? 0.0f : (q > levels ? levels : q);
         code[i] = static_cast<uint8_t>(q);
         const float step = scale * static_cast<float>(code[i]);
@@ -182,37 +191,34 @@ struct PackArgs {
 namespace {
 
 template <int DT, int G>
+// Grid (row tiles, batch, tensor): 16-lane groups (G lanes) own one output row each, so no
+// thread divides a linear index.
 __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
     constexpr int D = G * 8;
     const int sub = threadIdx.x % G;
-    const int64_t per_tensor = static_cast<int64_t>(a.batch) * a.length;
-    const int64_t rows = per_tensor * a.num;
-    for (int64_t r = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / G; r < rows;
-         r += static_cast<int64_t>(gridDim.x) * blockDim.x / G) {
-        const int ti = static_cast<int>(r / per_tensor);
-        const PackTensor& T = a.t[ti];
-        const int64_t row = r - ti * per_tensor;
-        const int64_t b = row / a.length;
-        const int j = static_cast<int>(row - b * a.length);
-        const int64_t dst = row * D + sub * 8;
-        if (j >= a.video) {
-            Row8<DT>::copy(T.input, dst, T.output, dst);
-            continue;
-        }
-        const int tok = T.indices[b * a.video + j];
-        const int64_t src = (b * a.length + tok) * D + sub * 8;
-        if (T.bits == 0) {
-            Row8<DT>::copy(T.input, src, T.output, dst);
-            continue;
-        }
-        const int lab = T.labels[b * a.video + tok];
-        float xv[8], cv[8], out[8], lo, sc;
-        uint8_t q[8];
-        Row8<DT>::load(T.input, src, xv);
-        load_centroid8(T.centroids + (b * T.clusters + lab) * D + sub * 8, cv);
-        base_offset_lane<G>(xv, cv, static_cast<float>((1 << T.bits) - 1), out, q, lo, sc);
-        Row8<DT>::store(T.output, dst, out);
+    const int j = static_cast<int>(blockIdx.x) * (256 / G) + static_cast<int>(threadIdx.x) / G;
+    if (j >= a.length) return;
+    const int64_t b = blockIdx.y;
+    const PackTensor& T = a.t[blockIdx.z];
+    const int64_t row = b * a.length + j;
+    const int64_t dst = row * D + sub * 8;
+    if (j >= a.video) {
+        Row8<DT>::copy(T.input, dst, T.output, dst);
+        return;
     }
+    const int tok = T.indices[b * a.video + j];
+    const int64_t src = (b * a.length + tok) * D + sub * 8;
+    if (T.bits == 0) {
+        Row8<DT>::copy(T.input, src, T.output, dst);
+        return;
+    }
+    const int lab = T.labels[b * a.video + tok];
+    float xv[8], cv[8], out[8], lo, sc;
+    uint8_t q[8];
+    Row8<DT>::load(T.input, src, xv);
+    load_centroid8(T.centroids + (b * T.clusters + lab) * D + sub * 8, cv);
+    base_offset_lane<G>(xv, cv, static_cast<float>((1 << T.bits) - 1), out, q, lo, sc);
+    Row8<DT>::store(T.output, dst, out);
 }
 
 int grid_for_rows(int64_t rows, int G) {
@@ -242,7 +248,6 @@ bool dispatch_dt_g(int dtype, int dims, int64_t rows, hipStream_t s, Args... arg
 
 template <int DT, int G> struct EncodeK { static constexpr auto kernel = base_offset_kernel<DT, G>; };
 template <int DT, int G> struct DecodeK { static constexpr auto kernel = base_offset_decode_kernel<DT, G>; };
-template <int DT, int G> struct PackK { static constexpr auto kernel = pack_kernel<DT, G>; };
 
 bool valid_quant_args(int batch, int tokens, int clusters, int dims) {
     return batch >= 1 && tokens >= 1 && clusters >= 1 && (dims == 64 || dims == 128);
@@ -312,7 +317,20 @@ PECO_API int peco_pack_clustered(const void* const* inputs, void* const* outputs
         if (bits[i] != 0 && (!labels[i] || !centroids[i] || clusters[i] < 1)) return kInvalidValue;
         a.t[i] = PackTensor{inputs[i], outputs[i], indices[i], labels[i], centroids[i], clusters[i], bits[i]};
     }
-    const int64_t rows = static_cast<int64_t>(num_tensors) * batch * length;
-    if (!dispatch_dt_g<PackK>(dtype, dims, rows, static_cast<hipStream_t>(stream), a)) return kUnsupportedDtype;
+    if (batch > 65535) return kUnsupportedShape;
+    const int G = dims / 8;
+    const dim3 grid(static_cast<unsigned>(ceil_div(length, 256 / G)), static_cast<unsigned>(batch),
+                    static_cast<unsigned>(num_tensors));
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+#define PECO_PACK(DT_)                                                                   \
+    do {                                                                                 \
+        if (G == 16) hipLaunchKernelGGL((pack_kernel<DT_, 16>), grid, dim3(256), 0, s, a); \
+        else hipLaunchKernelGGL((pack_kernel<DT_, 8>), grid, dim3(256), 0, s, a);          \
+    } while (0)
+    if (dtype == kBF16) PECO_PACK(kBF16);
+    else if (dtype == kF16) PECO_PACK(kF16);
+    else if (dtype == kF32) PECO_PACK(kF32);
+    else return kUnsupportedDtype;
+#undef PECO_PACK
     return hipGetLastError();
 }

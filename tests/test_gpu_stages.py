@@ -99,6 +99,34 @@ def test_base_offset_bit_exact(announce, dtype, bits, dims):
     assert _bits_equal(reference_path.fake_quantize(x, labels, cent, bits), ref_hat)
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("dims", [128, 64])
+def test_base_offset_half_integer_quotients(announce, bits, dims):
+    """Residual/scale quotients exactly on a half-integer (round half to even decides) and one
+    ulp either side of it, where a reciprocal-based quotient could round the other way."""
+    g = _gen(bits + dims + 1)
+    bh, n = 2, 256
+    levels = (1 << bits) - 1
+    lo = (torch.randint(-64, 64, (bh, n, 1), generator=g).float() / 8)
+    s = 2.0 ** torch.randint(-6, 3, (bh, n, 1), generator=g).float()       # exact scale: span / levels
+    k = torch.randint(0, levels, (bh, n, dims), generator=g).float()
+    x = lo + (k + 0.5) * s                                                  # quotient k + 0.5 exactly
+    nudge = torch.randint(-1, 2, (bh, n, dims), generator=g)               # -1, 0, +1 ulp
+    x = torch.where(nudge == 0, x, torch.nextafter(x, x + nudge.float() * torch.inf))
+    x[..., 0:1] = lo                                                        # row minimum
+    x[..., 1:2] = lo + levels * s                                           # row maximum (span = levels * s)
+    cent = torch.zeros(bh, 1, dims)
+    labels = torch.zeros(bh, n, dtype=torch.int32)
+    announce(f"bits={bits} D={dims}")
+    enc = quantization.quantize_base_offset(x.to(DEV), labels.to(DEV), cent.to(DEV), bits)
+    codes, low, scale, xhat = canonical.base_offset(x.numpy(), labels.numpy(), cent.numpy(), bits)
+    assert np.array_equal(enc.codes.cpu().numpy(), codes)
+    assert np.array_equal(enc.scale.cpu().numpy()[..., 0].view(np.int32), scale.view(np.int32))
+    assert _bits_equal(enc.dequantize().cpu(), torch.from_numpy(xhat))
+    # Ties really occur (codes at both neighbours of a half-integer).
+    assert (torch.from_numpy(codes.astype(np.int64)) % 2 == 0).any() and (torch.from_numpy(codes.astype(np.int64)) % 2 == 1).any()
+
+
 @pytest.mark.parametrize("bits", [0, 4])
 def test_pack_matches_quant_gather_concat(announce, bits):
     g = _gen(bits + 100)
