@@ -611,9 +611,29 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
         }
         __builtin_amdgcn_sched_barrier(0);
         after_s();
+        auto read_vt = [&](int cb, int kk, int nb) __attribute__((always_inline)) {
+            s16x4 part[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int vrow = 32 * cb + 16 * kk + 8 * t + 4 * h + src / 4;
+                const int d = 32 * nb + 16 * gsub + 4 * (src % 4);
+                const int pc = (d / 8) ^ T::swz_v(vrow);
+                const uint16_t* a = vt + vrow * D + pc * 8 + (d % 8);
+                part[t] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(a));
+            }
+            return __builtin_bit_cast(
+                u16x8, u32x4{__builtin_bit_cast(u32x2, part[0])[0], __builtin_bit_cast(u32x2, part[0])[1],
+                             __builtin_bit_cast(u32x2, part[1])[0], __builtin_bit_cast(u32x2, part[1])[1]});
+        };
 #pragma unroll
         for (int j = 0; j < NCB; ++j) {
             const int cb = cb0 + j;
+            // The V^T fragments of the first 16-key step are read before the softmax, whose
+            // VALU work then covers their LDS latency.
+            u16x8 vpre[NB];
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) vpre[nb] = read_vt(cb, 0, nb);
+            __builtin_amdgcn_sched_barrier(0);
             if (partial) {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
@@ -621,11 +641,14 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
                     if (key >= L) sacc[j][i] = -INFINITY;
                 }
             }
+            // Lanes l and l ^ 32 hold the two key halves of one query column and share m_run,
+            // so some lane's own maximum passes m_run + lazy exactly when some column's
+            // maximum does: the exchange of the halves is needed only to rescale.
             float tmax = sacc[j][0];
 #pragma unroll
             for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, sacc[j][i]);
-            tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
             if (__any(tmax > m_run + lazy)) {
+                tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
                 const float m_new = fmaxf(m_run, tmax);
                 const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
                 m_run = m_new;
@@ -654,19 +677,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
                                                                 pp[4 * kk + 3]});
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb) {
-                    s16x4 part[2];
-#pragma unroll
-                    for (int t = 0; t < 2; ++t) {
-                        const int vrow = 32 * cb + 16 * kk + 8 * t + 4 * h + src / 4;
-                        const int d = 32 * nb + 16 * gsub + 4 * (src % 4);
-                        const int pc = (d / 8) ^ T::swz_v(vrow);
-                        const uint16_t* a = vt + vrow * D + pc * 8 + (d % 8);
-                        part[t] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                            (__attribute__((address_space(3))) s16x4*)(a));
-                    }
-                    const u16x8 af = __builtin_bit_cast(
-                        u16x8, u32x4{__builtin_bit_cast(u32x2, part[0])[0], __builtin_bit_cast(u32x2, part[0])[1],
-                                     __builtin_bit_cast(u32x2, part[1])[0], __builtin_bit_cast(u32x2, part[1])[1]});
+                    const u16x8 af = kk == 0 ? vpre[nb] : read_vt(cb, kk, nb);
                     oacc[nb] = Mfma<DT>::run(af, pf, oacc[nb]);
                 }
             }
