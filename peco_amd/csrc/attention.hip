@@ -494,10 +494,16 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     const int ntiles = static_cast<int>(ceil_div(L, kKTile));
     // Physical row of stream row r (r < L). Every lane asks for increasing rows (its row of
     // every tile), so a forward-only cursor over the segments suffices.
-    int cur = 0;
+    // The current segment's row delta and end stay in registers; the segment table is read
+    // only when a row crosses into a later segment.
+    int cur = 0, seg_x = kseg[0].x, seg_end = nk > 0 ? kseg[1].y : 0x7fffffff;
     auto row_of = [&](int r) {
-        while (kseg[cur + 1].y <= r) ++cur;
-        return r + kseg[cur].x;
+        while (seg_end <= r) {
+            ++cur;
+            seg_x = kseg[cur].x;
+            seg_end = kseg[cur + 1].y;
+        }
+        return r + seg_x;
     };
     // Tile rows move through a pipeline. Lane l of wave w follows tile row 16*w + l%16 (lanes
     // 0..15 own it, the others shadow it). During tile t it issues the direct-to-LDS loads of
