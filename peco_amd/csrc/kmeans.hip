@@ -369,6 +369,11 @@ __global__ __launch_bounds__(kAssignThreads, 2) void km_assign_kernel(KmArgs a, 
     // Sorted kTop smallest screened values per token and lane half (t[0] <= t[1] <= ...). The centre index
     // j is packed into the low `ibits` mantissa bits, so min/med3 track value and index
     // together; the packing error is part of the certification bound below.
+    // -inf in an SGPR the compiler cannot see through: med3(t, v, -inf) = min(t, v) stays a
+    // single v_med3_f32 instead of becoming a min with NaN-quieting of both operands.
+    uint32_t neg_inf_bits;
+    asm volatile("s_mov_b32 %0, 0xff800000" : "=s"(neg_inf_bits));
+    const float neg_inf = __uint_as_float(neg_inf_bits);
     const int ibits = 32 - __builtin_clz(static_cast<unsigned>(max(K - 1, 1)));
     const uint32_t imask = (1u << ibits) - 1u;
     float t[2][kTop];
@@ -414,7 +419,7 @@ __global__ __launch_bounds__(kAssignThreads, 2) void km_assign_kernel(KmArgs a, 
                 const float v = __uint_as_float((__float_as_uint(acc[c][i]) & ~imask) | j);
 #pragma unroll
                 for (int k = kTop - 1; k > 0; --k) t[c][k] = __builtin_amdgcn_fmed3f(t[c][k - 1], v, t[c][k]);
-                t[c][0] = fminf(t[c][0], v);
+                t[c][0] = __builtin_amdgcn_fmed3f(t[c][0], v, neg_inf);
             }
         }
     };
