@@ -122,3 +122,37 @@ def test_layer_warm_start_second_step(announce):
         assert err.mean().item() <= 2e-3
         assert err.max().item() <= 2e-2
         q_init, k_init = torch.from_numpy(qc), torch.from_numpy(kc)
+
+
+def test_layer_full_size_heads_independent(announce):
+    """The 480p layer at its full size (24 heads). Heads share nothing, so the first two heads
+    of the 24-head call equal a call on those two heads alone, bit for bit (output and sort
+    permutations); every head's permutation is a permutation of its video tokens; and head 0
+    matches the oracle."""
+    wl = workloads.make_workload("hunyuan_480p")
+    iters = wl.shape.iterations
+    n = wl.shape.video
+    announce(f"hunyuan_480p full size: heads={wl.shape.heads} video={n} iters={iters}")
+    layer, out = _run_layer(wl, iters)
+    q_idx, k_idx = (t.cpu() for t in layer._last_fit)
+    ar = torch.arange(n, dtype=q_idx.dtype)
+    for idx in (q_idx, k_idx):
+        assert idx.shape == (wl.shape.heads, n)
+        assert torch.equal(idx.sort(dim=-1).values, ar.expand(wl.shape.heads, n))
+    assert torch.isfinite(out.float()).all()
+
+    def heads(w, sel):
+        shape = workloads.LayerShape(**{**w.shape.__dict__, "heads": len(sel)})
+        return workloads.Workload(shape, w.query[:, sel].contiguous(), w.key[:, sel].contiguous(),
+                                  w.value[:, sel].contiguous(), w.q_init[sel].contiguous(), w.k_init[sel].contiguous())
+
+    part = heads(wl, [0, 1])
+    layer2, out2 = _run_layer(part, iters)
+    assert torch.equal(out[:, :2].cpu(), out2.cpu())
+    assert torch.equal(q_idx[:2], layer2._last_fit[0].cpu())
+    assert torch.equal(k_idx[:2], layer2._last_fit[1].cpu())
+    ref, _ = _oracle_layer(heads(wl, [0]), iters)
+    err = (out[:, :1].float().cpu() - ref.float()).abs()
+    print(f"[full] head 0: max {err.max().item():.3e} mean {err.mean().item():.3e}", flush=True)
+    assert err.mean().item() <= 2e-3
+    assert err.max().item() <= 2e-2
