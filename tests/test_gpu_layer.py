@@ -10,12 +10,13 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 
 
-def _run_layer(wl, iterations):
+def _run_layer(wl, iterations, valid_text=None):
     shape = wl.shape
+    valid_text = shape.text if valid_text is None else valid_text
     cfg = processor.PecoConfig(num_q_centroids=shape.num_q_centroids, num_k_centroids=shape.num_k_centroids,
                                top_p=wl.top_p, min_kc_ratio=wl.min_kc_ratio, kmeans_iter_init=iterations,
                                kmeans_iter_step=iterations, warmup_steps=0, base_offset_bits=shape.bits)
-    ctx = processor.InferenceContext(step=0, text_length=shape.text, valid_text_length=shape.text)
+    ctx = processor.InferenceContext(step=0, text_length=shape.text, valid_text_length=valid_text)
     layer = processor.PecoAttention(0, cfg, ctx)
     layer.q_centroids, layer.k_centroids = wl.q_init.to(DEV), wl.k_init.to(DEV)
     with torch.no_grad():
@@ -24,8 +25,9 @@ def _run_layer(wl, iterations):
     return layer, out
 
 
-def _oracle_layer(wl, iterations):
+def _oracle_layer(wl, iterations, valid_text=None):
     shape = wl.shape
+    valid_text = shape.text if valid_text is None else valid_text
 
     def attend(q, k, v, m, qs, ks):
         o = canonical.sparse_attention(q[0].float().numpy(), k[0].float().numpy(), v[0].float().numpy(),
@@ -40,7 +42,7 @@ def _oracle_layer(wl, iterations):
     out = reference_path.peco_layer(
         wl.query, wl.key, wl.value, num_q_centroids=shape.num_q_centroids, num_k_centroids=shape.num_k_centroids,
         iterations=iterations, q_init=wl.q_init, k_init=wl.k_init, top_p=wl.top_p, min_kc_ratio=wl.min_kc_ratio,
-        bits=shape.bits, text_length=shape.text, valid_text=shape.text, attention=attend, fit=fit, stages=stages)
+        bits=shape.bits, text_length=shape.text, valid_text=valid_text, attention=attend, fit=fit, stages=stages)
     return out, stages
 
 
@@ -154,5 +156,28 @@ def test_layer_full_size_heads_independent(announce):
     ref, _ = _oracle_layer(heads(wl, [0]), iters)
     err = (out[:, :1].float().cpu() - ref.float()).abs()
     print(f"[full] head 0: max {err.max().item():.3e} mean {err.mean().item():.3e}", flush=True)
+    assert err.mean().item() <= 2e-3
+    assert err.max().item() <= 2e-2
+
+
+@pytest.mark.parametrize("name,dtype,pad", [
+    ("hunyuan_480p", torch.bfloat16, 100),
+    ("hunyuan_480p_bo4", torch.float16, 37),
+    ("hunyuan_480p", torch.float16, 0),
+    ("hunyuan_480p_bo4", torch.bfloat16, 256),
+])
+def test_layer_padded_text_and_fp16(announce, name, dtype, pad):
+    """Text padding (valid_text < text length: the padding rows attend only to themselves, the
+    valid text and video never to them) and fp16 inputs, end to end against the oracle."""
+    wl = workloads.make_workload(name, heads=1, video=4096)
+    wl = workloads.Workload(wl.shape, wl.query.to(dtype), wl.key.to(dtype), wl.value.to(dtype), wl.q_init, wl.k_init)
+    valid = wl.shape.text - pad
+    iters = wl.shape.iterations
+    announce(f"{name} {dtype} video=4096 text={wl.shape.text} valid_text={valid}")
+    layer, out = _run_layer(wl, iters, valid_text=valid)
+    ref, _ = _oracle_layer(wl, iters, valid_text=valid)
+    assert out.dtype == dtype
+    err = (out.float().cpu() - ref.float()).abs()
+    print(f"[padded] {name} {dtype} valid {valid}: max {err.max().item():.3e} mean {err.mean().item():.3e}", flush=True)
     assert err.mean().item() <= 2e-3
     assert err.max().item() <= 2e-2
