@@ -402,6 +402,11 @@ def main():
         "stages_ms": {k_: round(v_, 4) for k_, v_ in stages.items()},
         "layer_frac_of_peak": round(value / PEAK_BF16_TFLOPS, 4),
     }
+    # Stage 1 on its own: F1 = 2*D*N*(KQ+KK)*BH*iterations useful FLOPs over the fit's stage time.
+    f1 = 2.0 * s.dims * s.video * (s.num_q_centroids + s.num_k_centroids) * s.heads * s.iterations
+    if stages.get("kmeans"):
+        t1 = f1 / (stages["kmeans"] * 1e-3) / 1e12
+        line["kmeans_fit"] = {"flops": f1, "tflops": round(t1, 2), "frac_of_peak": round(t1 / PEAK_BF16_TFLOPS, 4)}
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds)
     print(json.dumps(line), flush=True)
