@@ -3,8 +3,9 @@
 // The permutation is the stable argsort of labels per batch entry
 // (peco/clustering.py:105, torch.argsort(..., stable=True)), computed as a counting sort:
 //   1. sort_hist:  per 256-token tile, a label histogram (LDS atomics; counts only).
-//   2. sort_scan:  per batch entry, scan tiles per cluster and clusters -> absolute
-//                  start position of each (tile, cluster) run, counts and offsets.
+//   2. sort_scan_groups + sort_scan: reduce-then-scan of the tile counts -> per (tile,
+//                  cluster) run its exclusive prefix within a group of kScanTiles tiles,
+//                  per (group, cluster) its absolute start, counts and offsets.
 //   3. sort_place: per tile, one wavefront ranks 64 tokens per step. Lanes holding the
 //                  same label are found with one ballot per label bit (no serial match
 //                  loop); the rank among equal labels is a popcount of lower lanes, so
@@ -59,6 +60,17 @@ __device__ __forceinline__ int find_problem_by_batch(const SortArgs& a, int b) {
     return p;
 }
 
+__device__ __forceinline__ int find_problem_by_scan_group(const SortArgs& a, int g) {
+    int p = 0;
+    while (p + 1 < a.num && g >= a.p[p + 1].scan_group_begin) ++p;
+    return p;
+}
+
+// [batch, scan groups, clusters] area behind the tile histograms.
+__device__ __forceinline__ int32_t* scan_group_area(const SortProblem& P) {
+    return P.tile_hist + static_cast<int64_t>(P.batch) * P.tiles * P.clusters;
+}
+
 __global__ __launch_bounds__(256) void sort_hist_kernel(SortArgs args) {
     extern __shared__ int hist[];
     const int pi = find_problem_by_block(args, blockIdx.x);
@@ -80,6 +92,40 @@ __global__ __launch_bounds__(256) void sort_hist_kernel(SortArgs args) {
     for (int k = threadIdx.x; k < P.clusters; k += blockDim.x) out[k] = hist[k];
 }
 
+// Phase 1 of the scan: per group of kScanTiles tiles, each (tile, cluster) count becomes its
+// exclusive prefix within the group (in place) and the group's cluster totals go to the
+// group area. A cluster's whole group column is loaded before any of it is written.
+__global__ __launch_bounds__(256) void sort_scan_groups_kernel(SortArgs args) {
+    const int pi = find_problem_by_scan_group(args, blockIdx.x);
+    const SortProblem& P = args.p[pi];
+    const int local = blockIdx.x - P.scan_group_begin;
+    const int b = local / P.scan_groups;
+    const int g = local % P.scan_groups;
+    const int K = P.clusters;
+    const int t0 = g * kScanTiles;
+    const int nt = min(kScanTiles, P.tiles - t0);
+    int32_t* th = P.tile_hist + (static_cast<int64_t>(b) * P.tiles + t0) * K;
+    int32_t* gt = scan_group_area(P) + (static_cast<int64_t>(b) * P.scan_groups + g) * K;
+    for (int k = threadIdx.x; k < K; k += blockDim.x) {
+        int c[kScanTiles];
+#pragma unroll
+        for (int u = 0; u < kScanTiles; ++u) {
+            // Clamped unconditional loads (masked after) stay in flight together.
+            const int v = th[static_cast<int64_t>(min(u, nt - 1)) * K + k];
+            c[u] = u < nt ? v : 0;
+        }
+        int run = 0;
+#pragma unroll
+        for (int u = 0; u < kScanTiles; ++u) {
+            if (u < nt) th[static_cast<int64_t>(u) * K + k] = run;
+            run += c[u];
+        }
+        gt[k] = run;
+    }
+}
+
+// Phase 2, per batch entry: cluster totals from the group totals, their exclusive scan
+// (offsets, counts), and each (group, cluster) total replaced by the group's absolute start.
 __global__ __launch_bounds__(256) void sort_scan_kernel(SortArgs args) {
     extern __shared__ int cnt[];
     __shared__ int tmp[4];
@@ -87,19 +133,18 @@ __global__ __launch_bounds__(256) void sort_scan_kernel(SortArgs args) {
     const SortProblem& P = args.p[pi];
     const int b = blockIdx.x - P.batch_begin;
     const int K = P.clusters;
-    const int tiles = P.tiles;
-    int32_t* th = P.tile_hist + static_cast<int64_t>(b) * tiles * K;
-    constexpr int kBatch = 8;  // tile counts in flight per thread
+    const int groups = P.scan_groups;
+    int32_t* gt = scan_group_area(P) + static_cast<int64_t>(b) * groups * K;
+    constexpr int kBatch = 8;  // group totals in flight per thread
     // Pass 1 (loads only): total count of each cluster.
     for (int k = threadIdx.x; k < K; k += blockDim.x) {
         int run = 0;
-        for (int t0 = 0; t0 < tiles; t0 += kBatch) {
+        for (int g0 = 0; g0 < groups; g0 += kBatch) {
             int c[kBatch];
 #pragma unroll
             for (int u = 0; u < kBatch; ++u) {
-                // Clamped unconditional loads (masked after) stay in flight together.
-                const int v = th[static_cast<int64_t>(min(t0 + u, tiles - 1)) * K + k];
-                c[u] = t0 + u < tiles ? v : 0;
+                const int v = gt[static_cast<int64_t>(min(g0 + u, groups - 1)) * K + k];
+                c[u] = g0 + u < groups ? v : 0;
             }
 #pragma unroll
             for (int u = 0; u < kBatch; ++u) run += c[u];
@@ -126,20 +171,20 @@ __global__ __launch_bounds__(256) void sort_scan_kernel(SortArgs args) {
     }
     if (threadIdx.x == 0) off[K] = total;
     __syncthreads();
-    // Pass 2: each (tile, cluster) count becomes the absolute start of that run. A batch of
-    // counts is read before any of it is overwritten.
+    // Pass 2: each (group, cluster) total becomes the absolute start of that group's runs. A
+    // batch of totals is read before any of it is overwritten.
     for (int k = threadIdx.x; k < K; k += blockDim.x) {
         int pos = cnt[k];
-        for (int t0 = 0; t0 < tiles; t0 += kBatch) {
+        for (int g0 = 0; g0 < groups; g0 += kBatch) {
             int c[kBatch];
 #pragma unroll
             for (int u = 0; u < kBatch; ++u) {
-                const int v = th[static_cast<int64_t>(min(t0 + u, tiles - 1)) * K + k];
-                c[u] = t0 + u < tiles ? v : 0;
+                const int v = gt[static_cast<int64_t>(min(g0 + u, groups - 1)) * K + k];
+                c[u] = g0 + u < groups ? v : 0;
             }
 #pragma unroll
             for (int u = 0; u < kBatch; ++u) {
-                if (t0 + u < tiles) th[static_cast<int64_t>(t0 + u) * K + k] = pos;
+                if (g0 + u < groups) gt[static_cast<int64_t>(g0 + u) * K + k] = pos;
                 pos += c[u];
             }
         }
@@ -157,12 +202,15 @@ __global__ __launch_bounds__(64) void sort_place_kernel(SortArgs args) {
     const int lane = threadIdx.x;
     const int32_t* th = P.tile_hist + (static_cast<int64_t>(b) * P.tiles + tile) * K;
     int32_t* th_mut = P.tile_hist + (static_cast<int64_t>(b) * P.tiles + tile) * K;
-    // Run starts of this tile (four loads in flight per lane before any store).
+    const int32_t* gs = scan_group_area(P) + (static_cast<int64_t>(b) * P.scan_groups + tile / kScanTiles) * K;
+    // Run starts of this tile: the in-group prefix plus the group's start (four of each in
+    // flight per lane before any store).
     for (int k0 = 0; k0 < K; k0 += 4 * kWave) {
         int v[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const int x = th[min(k0 + u * kWave + lane, K - 1)];
+            const int e = min(k0 + u * kWave + lane, K - 1);
+            const int x = th[e] + gs[e];
             v[u] = k0 + u * kWave + lane < K ? x : 0;
         }
 #pragma unroll
@@ -363,19 +411,23 @@ __global__ __launch_bounds__(256) void reorder_rows_kernel(const T* __restrict__
 }  // namespace
 
 void sort_args_finalize(SortArgs& a) {
-    int blocks = 0, batches = 0, groups = 0;
+    int blocks = 0, batches = 0, groups = 0, scan_groups = 0;
     for (int i = 0; i < a.num; ++i) {
         a.p[i].tiles = sort_tiles(a.p[i].tokens);
+        a.p[i].scan_groups = sort_scan_groups(a.p[i].tokens);
         a.p[i].block_begin = blocks;
         a.p[i].batch_begin = batches;
         a.p[i].group_begin = groups;
+        a.p[i].scan_group_begin = scan_groups;
         blocks += a.p[i].batch * a.p[i].tiles;
         batches += a.p[i].batch;
         groups += a.p[i].batch * static_cast<int>(ceil_div(a.p[i].tiles, kFusedTiles));
+        scan_groups += a.p[i].batch * a.p[i].scan_groups;
     }
     a.total_blocks = blocks;
     a.total_batches = batches;
     a.total_groups = groups;
+    a.total_scan_groups = scan_groups;
 }
 
 hipError_t launch_cluster_sort(const SortArgs& args, hipStream_t stream, bool with_hist) {
@@ -390,6 +442,7 @@ hipError_t launch_cluster_sort(const SortArgs& args, hipStream_t stream, bool wi
         return hipGetLastError();
     }
     if (with_hist) hipLaunchKernelGGL(sort_hist_kernel, dim3(args.total_blocks), dim3(256), lds, stream, args);
+    hipLaunchKernelGGL(sort_scan_groups_kernel, dim3(args.total_scan_groups), dim3(256), 0, stream, args);
     hipLaunchKernelGGL(sort_scan_kernel, dim3(args.total_batches), dim3(256), lds, stream, args);
     hipLaunchKernelGGL(sort_place_kernel, dim3(args.total_blocks), dim3(64), lds, stream, args);
     return hipGetLastError();

@@ -22,6 +22,8 @@ struct SortProblem {
     int block_begin;        // first linear (batch, tile) block of this problem
     int batch_begin;        // first linear batch entry of this problem (scan grid)
     int group_begin;        // first linear (batch, tile group) workgroup (fused grid)
+    int scan_groups;        // groups of kScanTiles tiles per batch entry
+    int scan_group_begin;   // first linear (batch, scan group) workgroup (group scan grid)
 };
 
 constexpr int kMaxSortProblems = 2;
@@ -34,6 +36,7 @@ struct SortArgs {
     int zero_hist;      // sort_place clears each consumed tile histogram (for accumulating producers)
     int fused;          // one sort_fused launch instead of scan + place (sort_fusable problems only)
     int total_groups;   // sum of batch * ceil(tiles / kFusedTiles)
+    int total_scan_groups;  // sum of batch * scan_groups
 };
 
 // Fused sort: a workgroup ranks kFusedTiles consecutive tiles (one per wavefront) and derives
@@ -49,8 +52,18 @@ inline bool sort_fusable(int tokens, int clusters) {
 
 inline int sort_tiles(int tokens) { return static_cast<int>(ceil_div(tokens, kSortTile)); }
 
+// The unfused scan is a reduce-then-scan over groups of kScanTiles tiles: per group, the
+// (tile, cluster) counts become exclusive prefixes within the group and the group totals go
+// to a second area; per batch entry, the group totals are scanned into cluster offsets and
+// group starts; the place kernel adds its group's start to its in-group prefixes.
+constexpr int kScanTiles = 32;
+
+inline int sort_scan_groups(int tokens) { return static_cast<int>(ceil_div(sort_tiles(tokens), kScanTiles)); }
+
+// [batch, tiles, clusters] tile histograms followed by [batch, scan groups, clusters] group
+// totals.
 inline size_t sort_workspace_ints(int batch, int tokens, int clusters) {
-    return static_cast<size_t>(batch) * sort_tiles(tokens) * clusters;
+    return static_cast<size_t>(batch) * (sort_tiles(tokens) + sort_scan_groups(tokens)) * clusters;
 }
 
 // Fills block_begin/batch_begin/totals for problems[0..num).

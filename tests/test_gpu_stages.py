@@ -31,7 +31,9 @@ def _mixture(g, bh, n, d, m, sigma=1.0):
 
 # ---------------------------------------------------------------- stage 3: sort + reorder
 
-@pytest.mark.parametrize("clusters,tokens", [(1, 777), (7, 5000), (256, 6750), (1000, 3000), (64, 70)])
+# 40000 and 118800 tokens span several 32-tile scan groups (the last one partial).
+@pytest.mark.parametrize("clusters,tokens", [(1, 777), (7, 5000), (256, 6750), (1000, 3000), (64, 70), (300, 40000),
+                                             (1024, 118800)])
 def test_cluster_sort_matches_stable_argsort(announce, clusters, tokens):
     g = _gen(clusters * 31 + tokens)
     labels = torch.randint(clusters, (3, tokens), generator=g, dtype=torch.int32)
