@@ -7,9 +7,12 @@
 // Work list (one 256-thread workgroup per (batch*head)):
 //   cluster offsets are min(S, prefix of max(0, size)) (the reference's clamped running sum),
 //   each query cluster is cut into items of <= 128 rows, and the items of one head are
-//   ordered by descending cost rows * kept_keys. The attention grid is slot-major
-//   (block = slot * BH + bh): the costliest item of every head starts first, and with BH a
-//   multiple of 8 all items of one head land on one XCD, whose L2 then holds that head's K/V.
+//   ordered by descending cost rows * kept_keys. The attention grid is slot-major over bands
+//   of heads (block = band_index * band * cap + slot * band + head in band): the costliest
+//   item of every head of a band starts first. The band is all heads when their K/V fit in
+//   the MALL (then, with BH a multiple of 8, all items of one head land on one XCD, whose L2
+//   holds that head's K/V), else as many heads as fit, so long sequences stream each head's
+//   K/V from the MALL instead of HBM.
 //
 // Attention workgroup = one item: 4 waves x 32 query rows. The kept key clusters of the
 // item's query cluster form one virtual key stream (their rows are contiguous per cluster
@@ -438,8 +441,8 @@ template <int DT, int D, bool kIndexed>
 __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint8_t* __restrict__ selected, const int32_t* __restrict__ ws, uint16_t* __restrict__ out,
-    const int32_t* __restrict__ out_index, int oi_rows, const int32_t* __restrict__ k_index, int bhn, int sq,
-    int sk, int cq, int ck, float scale_log2) {
+    const int32_t* __restrict__ out_index, int oi_rows, const int32_t* __restrict__ k_index, int bhn, int band,
+    int sq, int sk, int cq, int ck, float scale_log2) {
     using T = Tiles<D>;
     constexpr int S = D / 16;       // k-steps of S^T over channels
     constexpr int NB = D / 32;      // 32-channel blocks of O^T
@@ -456,9 +459,12 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     // a sentinel whose offset no stream row reaches.
     int2* kseg = reinterpret_cast<int2*>(dyn);  // [ck + 1]
 
-    const int bh = blockIdx.x % bhn;
-    const int slot = blockIdx.x / bhn;
     const WorkLayout W = work_layout(const_cast<int32_t*>(ws), bhn, sq, cq, ck);
+    // Heads run in bands of `band` (a divisor of bhn), slot-major within a band.
+    const int per_band = band * W.cap;
+    const int in_band = blockIdx.x % per_band;
+    const int bh = (blockIdx.x / per_band) * band + in_band % band;
+    const int slot = in_band / band;
     if (slot >= W.counts[bh]) return;
     const int32_t* item = W.items + (static_cast<int64_t>(bh) * W.cap + slot) * 3;
     const int q_start = item[0], qc = item[1], q_rows = item[2];
@@ -801,6 +807,23 @@ PECO_API size_t peco_sparse_attention_workspace_size(int bh, int sq, int sk, int
 namespace peco {
 namespace {
 
+// Heads whose items run together. Every item of a head streams its K/V rows, so the K/V of the
+// heads in flight should stay in the 256 MB MALL. All heads form one band when their K/V fit
+// in kAllHeadsBytes (the grid is then slot-major over all heads and, with bh a multiple of 8,
+// every item of a head runs on one XCD); otherwise the band is the largest divisor of bh up
+// to kMaxBand whose K/V fit in the MALL (of bands of 1, 2, 4 and all 24 heads, 4 ran fastest
+// at both 32896 and 119056 tokens).
+constexpr double kAllHeadsBytes = 96.0 * 1024 * 1024;
+constexpr double kMallBytes = 256.0 * 1024 * 1024;
+constexpr int kMaxBand = 4;
+int attention_head_band(int bh, int sk, int d) {
+    const double kv = 4.0 * static_cast<double>(sk) * d;  // K and V bytes of one head (16-bit)
+    if (bh * kv <= kAllHeadsBytes) return bh;
+    for (int band = std::min(bh, kMaxBand); band > 1; --band)
+        if (bh % band == 0 && band * kv <= kMallBytes) return band;
+    return 1;
+}
+
 // Shared launcher: k_index (nullable) selects the indexed-input kernel (inputs in original
 // token order, read through out_index for Q and k_index for K/V).
 int launch_sparse_attention(const void* q, const void* k, const void* v, const uint8_t* selected,
@@ -828,13 +851,14 @@ int launch_sparse_attention(const void* q, const void* k, const void* v, const u
     const int cap = item_capacity(sq, cq);
     const float scale_log2 = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(d)));
     const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(cap) * bh));
+    const int band = attention_head_band(bh, sk, d);
     const auto* qp = static_cast<const uint16_t*>(q);
     const auto* kp = static_cast<const uint16_t*>(k);
     const auto* vp = static_cast<const uint16_t*>(v);
     auto* op = static_cast<uint16_t*>(output);
 #define PECO_ATTN(DT_, D_, IX_)                                                                                    \
     hipLaunchKernelGGL((sparse_attention_kernel<DT_, D_, IX_>), grid, dim3(256), lds_attn, s, qp, kp, vp, selected, \
-                       workspace, op, out_index, out_index_rows, k_index, bh, sq, sk, cq, ck, scale_log2)
+                       workspace, op, out_index, out_index_rows, k_index, bh, band, sq, sk, cq, ck, scale_log2)
 #define PECO_ATTN_D(DT_, IX_)                                                                                      \
     do {                                                                                                           \
         if (d == 128) PECO_ATTN(DT_, 128, IX_);                                                                    \

@@ -181,3 +181,19 @@ def test_layer_padded_text_and_fp16(announce, name, dtype, pad):
     print(f"[padded] {name} {dtype} valid {valid}: max {err.max().item():.3e} mean {err.mean().item():.3e}", flush=True)
     assert err.mean().item() <= 2e-3
     assert err.max().item() <= 2e-2
+
+
+def test_layer_head_bands_bit_exact(announce):
+    """At 119056 tokens the attention runs its 8 heads in two bands of 4 (one band's K/V fill
+    the MALL); a call on the first two heads runs them in one band. Heads are independent, so
+    the two calls agree bit for bit on those heads."""
+    wl = workloads.make_workload("hunyuan_720p", heads=8, device=DEV)
+    iters = 2
+    announce(f"hunyuan_720p heads=8 video={wl.shape.video} iters={iters}")
+    _, out = _run_layer(wl, iters)
+    shape = workloads.LayerShape(**{**wl.shape.__dict__, "heads": 2})
+    part = workloads.Workload(shape, wl.query[:, :2].contiguous(), wl.key[:, :2].contiguous(),
+                              wl.value[:, :2].contiguous(), wl.q_init[:2].contiguous(), wl.k_init[:2].contiguous())
+    _, out2 = _run_layer(part, iters)
+    assert torch.isfinite(out.float()).all()
+    assert torch.equal(out[:, :2], out2)
