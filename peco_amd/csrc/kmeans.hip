@@ -434,12 +434,21 @@ __global__ __launch_bounds__(kAssignThreads, 2) void km_assign_kernel(KmArgs a, 
         if (has2) load_centres<D>(regs, hi_base, lo_base, norms, (blk + 2) * 32, K, tid);
         screen((blk + 1) & 1, nxt);
         track(blk, cur);
-        constexpr int kMfma = S * 2 * (kSplitX ? 3 : 2);
+        // Per channel step s its MFMAs, each followed by a share of the tracking; the centre
+        // fragments of step s + kAhead are read after the first MFMA of step s, so LDS latency
+        // hides behind kAhead steps of MFMAs (the norms and the first kAhead steps' fragments
+        // are read up front).
+        constexpr int kPerS = 2 * (kSplitX ? 3 : 2);
+        constexpr int kAhead = 2;
+        __builtin_amdgcn_sched_group_barrier(0x100, 4 + 2 * kAhead, 0);
 #pragma unroll
-        for (int i = 0; i < kMfma; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, kTrackValuPerMfma, 0);
-        }
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int i = 0; i < kPerS; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if (i == 0 && s + kAhead < S) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, kTrackValuPerMfma, 0);
+            }
         // Uses of the candidate lists keep the tracking in this block (it would otherwise
         // be sunk past the barrier into the next block's tracking).
 #pragma unroll
