@@ -103,7 +103,7 @@ def stage_breakdown(layer, wl, q, k, v, q_init, k_init, reps):
             qp, kp, vp = clustering_cuda.pack_clustered([q, k, v], [q_idx, k_idx, k_idx], [ql, kl, None],
                                                         [layer.q_centroids, layer.k_centroids, None],
                                                         [s.bits, s.bits, 0], n)
-            attn_args = (qp, kp, vp, emap, eqs, eks, q_idx, None, n, None)
+            attn_args = (qp, kp, vp, emap, eqs, eks, q_idx, None, n, kept)
         ev[3].record()
         run_attention(attn_args)
         ev[4].record()
@@ -121,7 +121,7 @@ def run_attention(args_):
     q, k, v, emap, eqs, eks, q_idx, k_idx, rows, kept = args_
     if k_idx is None:
         return attention_cuda.sparse_attention(q, k, v, emap, eqs, eks, validate_sizes=False, out_index=q_idx,
-                                               out_index_rows=rows)
+                                               out_index_rows=rows, kept_keys=kept)
     return attention_cuda.sparse_attention_indexed(q, k, v, emap, eqs, eks, q_idx, k_idx, rows,
                                                    validate_sizes=False, kept_keys=kept)
 

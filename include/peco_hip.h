@@ -105,12 +105,15 @@ int peco_pack_clustered(const void* const* inputs, void* const* outputs, const i
 /* peco_sparse_attention with an explicit workspace size (int32 elements, at least
  * peco_sparse_attention_workspace_size) and an optional out_index [bh, out_index_rows]:
  * output row j < out_index_rows of head b is written to row out_index[b,j]; later rows keep
- * their position (fuses peco/clustering.py:128-136 and the text rows of processor.py:153-156). */
+ * their position (fuses peco/clustering.py:128-136 and the text rows of processor.py:153-156).
+ * kept_keys (nullable, int32 [bh, cq]) gives the key rows each query cluster keeps, as
+ * peco_select_cluster_connections writes them; it only orders the work items and spares the
+ * work-list builder its pass over the map. (ABI revision 2 added kept_keys.) */
 size_t peco_sparse_attention_workspace_size(int bh, int sq, int sk, int cq, int ck);
 int peco_sparse_attention_ex(const void* q, const void* k, const void* v, const uint8_t* selected,
                              const int* q_sizes, const int* k_sizes, void* output, const int32_t* out_index,
-                             int out_index_rows, int* workspace, size_t workspace_ints, int bh, int sq, int sk, int d,
-                             int cq, int ck, int dtype, void* stream);
+                             int out_index_rows, const int32_t* kept_keys, int* workspace, size_t workspace_ints,
+                             int bh, int sq, int sk, int d, int cq, int ck, int dtype, void* stream);
 
 /* peco_sparse_attention_ex on Q/K/V in their original token order: stream row j <
  * index_rows of head b reads query row q_index[b,j] and key/value row k_index[b,j], and output

@@ -120,7 +120,7 @@ SIGNATURES = {
     "peco_base_offset_fake_quant": (I, [P, I, P, P, I, I, I, I, I, P, P]),
     "peco_pack_clustered": (I, [PP, PP, PP, PP, PP, IP, IP, I, I, I, I, I, I, P]),
     "peco_sparse_attention_workspace_size": (Z, [I, I, I, I, I]),
-    "peco_sparse_attention_ex": (I, [P] * 8 + [I, P, Z] + [I] * 7 + [P]),
+    "peco_sparse_attention_ex": (I, [P] * 8 + [I, P, P, Z] + [I] * 7 + [P]),
     "peco_sparse_attention_indexed": (I, [P] * 9 + [I, P, P, Z] + [I] * 7 + [P]),
     "peco_select_cluster_connections": (I, [P] * 4 + [I] * 4 + [ctypes.c_float] + [I] * 4 + [P] * 5),
 }

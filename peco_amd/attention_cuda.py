@@ -100,8 +100,8 @@ def _launch(q, k, v, dynamic_map, q_sizes, k_sizes, validate_sizes, out_index, k
                 _native.ptr(k_sizes), _native.ptr(output))
         tail = (batch * heads, sq, sk, dim, cq, ck, dtype, stream)
         if k_index is None:
-            error = library.peco_sparse_attention_ex(*head, _native.ptr(out_index), rows, _native.ptr(workspace),
-                                                     workspace.numel(), *tail)
+            error = library.peco_sparse_attention_ex(*head, _native.ptr(out_index), rows, _native.ptr(kept_keys),
+                                                     _native.ptr(workspace), workspace.numel(), *tail)
         else:
             error = library.peco_sparse_attention_indexed(*head, _native.ptr(out_index), _native.ptr(k_index), rows,
                                                           _native.ptr(kept_keys), _native.ptr(workspace),
@@ -123,6 +123,7 @@ def sparse_attention(
     validate_sizes: bool = True,
     out_index: torch.Tensor | None = None,
     out_index_rows: int | None = None,
+    kept_keys: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Return cluster-masked softmax(QK^T/sqrt(D))V.
 
@@ -132,9 +133,12 @@ def sparse_attention(
     row returns zero. Sizes are checked on the stream without copying them to the host.
     ``out_index`` (int32 [B*H, R], optional) writes output row j < R of head b to row
     out_index[b, j] instead (rows j >= R keep their position), fusing the inverse token
-    permutation into the epilogue. R is ``out_index_rows`` (default SQ).
+    permutation into the epilogue. R is ``out_index_rows`` (default SQ). ``kept_keys`` (int32
+    [B,H,CQ], optional) gives the key rows each query cluster keeps, as
+    ``select_connections(..., with_kept=True)`` returns them; it only orders the work items.
     """
-    return _launch(q, k, v, dynamic_map, q_sizes, k_sizes, validate_sizes, out_index, None, out_index_rows)
+    return _launch(q, k, v, dynamic_map, q_sizes, k_sizes, validate_sizes, out_index, None, out_index_rows,
+                   kept_keys)
 
 
 def sparse_attention_indexed(

@@ -884,10 +884,11 @@ int launch_sparse_attention(const void* q, const void* k, const void* v, const u
 // position), fusing the inverse permutation into the epilogue.
 PECO_API int peco_sparse_attention_ex(const void* q, const void* k, const void* v, const uint8_t* selected,
                                       const int* q_sizes, const int* k_sizes, void* output, const int32_t* out_index,
-                                      int out_index_rows, int* workspace, size_t workspace_ints, int bh, int sq,
-                                      int sk, int d, int cq, int ck, int dtype, void* stream) {
+                                      int out_index_rows, const int32_t* kept_keys, int* workspace,
+                                      size_t workspace_ints, int bh, int sq, int sk, int d, int cq, int ck, int dtype,
+                                      void* stream) {
     return launch_sparse_attention(q, k, v, selected, q_sizes, k_sizes, output, out_index, out_index_rows, nullptr,
-                                   nullptr, workspace, workspace_ints, bh, sq, sk, d, cq, ck, dtype, stream);
+                                   kept_keys, workspace, workspace_ints, bh, sq, sk, d, cq, ck, dtype, stream);
 }
 
 // Gathering entry: q, k, v (and output) stay in original token order. The first index_rows
@@ -913,6 +914,6 @@ PECO_API int peco_sparse_attention(const void* q, const void* k, const void* v, 
                                    int sq, int sk, int d, int cq, int ck, int dtype, void* stream) {
     if (bh < 1 || sq < 0) return kInvalidValue;
     const size_t ref_ints = static_cast<size_t>(bh) * (ck + 2 + 3 * (ceil_div(sq, 16) + cq));
-    return peco_sparse_attention_ex(q, k, v, selected, q_sizes, k_sizes, output, nullptr, 0, workspace, ref_ints, bh,
-                                    sq, sk, d, cq, ck, dtype, stream);
+    return peco_sparse_attention_ex(q, k, v, selected, q_sizes, k_sizes, output, nullptr, 0, nullptr, workspace,
+                                    ref_ints, bh, sq, sk, d, cq, ck, dtype, stream);
 }

@@ -211,7 +211,7 @@ class PecoAttention:
             [self.q_centroids, self.k_centroids, None], [bits, bits, 0], video_length)
         # Video rows return to their original positions; text rows keep theirs.
         return sparse_attention(q_perm, k_perm, v_perm, dynamic_map, q_sizes, k_sizes, validate_sizes=False,
-                                out_index=q_idx, out_index_rows=video_length)
+                                out_index=q_idx, out_index_rows=video_length, kept_keys=kept)
 
     @torch.no_grad()
     def __call__(self, attn, hidden_states, encoder_hidden_states=None, attention_mask=None, image_rotary_emb=None):

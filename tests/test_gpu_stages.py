@@ -348,6 +348,13 @@ def test_sparse_attention_out_index_scatter(announce):
     fused = attention_cuda.sparse_attention(*args, out_index=perm.to(DEV))
     restored = clustering.restore_sequence_order(plain, perm.to(DEV))
     assert torch.equal(fused.cpu().view(torch.int16), restored.cpu().view(torch.int16))
+    # kept_keys only orders the work items (here against their true costs), so the result is
+    # the same bit for bit, with and without out_index.
+    kept = torch.tensor([[[1, 2], [300, 0]]], dtype=torch.int32).to(DEV)
+    ordered = attention_cuda.sparse_attention(*args, out_index=perm.to(DEV), kept_keys=kept)
+    assert torch.equal(ordered.cpu().view(torch.int16), fused.cpu().view(torch.int16))
+    assert torch.equal(attention_cuda.sparse_attention(*args, kept_keys=kept).cpu().view(torch.int16),
+                       plain.cpu().view(torch.int16))
 
 
 def _gather_rows(x, index):
