@@ -9,10 +9,10 @@
 //   each query cluster is cut into items of <= 128 rows, and the items of one head are
 //   ordered by descending cost rows * kept_keys. The attention grid is slot-major over bands
 //   of heads (block = band_index * band * cap + slot * band + head in band): the costliest
-//   item of every head of a band starts first. The band is all heads when their K/V fit in
-//   the MALL (then, with BH a multiple of 8, all items of one head land on one XCD, whose L2
-//   holds that head's K/V), else as many heads as fit, so long sequences stream each head's
-//   K/V from the MALL instead of HBM.
+//   item of every head of a band starts first. The band is all heads when their K/V take at
+//   most 96 MB (then, with BH a multiple of 8, all items of one head land on one XCD, whose L2
+//   holds that head's K/V), else up to four heads whose K/V fit in the MALL, so long
+//   sequences re-read each head's K/V from the MALL instead of HBM.
 //
 // Attention workgroup = one item: 4 waves x 32 query rows. The kept key clusters of the
 // item's query cluster form one virtual key stream (their rows are contiguous per cluster
