@@ -22,7 +22,9 @@ extern "C" {
 
 /* Replaces peco_assign_tokens_to_centers, peco/kernels/kmeans.cu:139.
  * labels[b,t] = argmin_j fma(-2, x_t.c_j, |c_j|^2), lowest j on ties (fixed-order fp32).
- * center_norms (nullable) receives |c_j|^2. scratch/chunk_size are accepted and unused. */
+ * center_norms [batch, clusters] receives |c_j|^2; when it is null the first batch*clusters
+ * floats of scratch hold them (one of the two must be given). chunk_size is unused.
+ * Allocates nothing. */
 int peco_assign_tokens_to_centers(const float* x, const float* centers, int32_t* labels, float* scratch,
                                   float* center_norms, int batch, int tokens, int dims, int clusters,
                                   int chunk_size, void* stream);

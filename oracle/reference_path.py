@@ -223,3 +223,64 @@ def peco_layer(query, key, value, *, num_q_centroids, num_k_centroids, iteration
                       q_indices=q_idx, k_indices=k_idx, q_perm=q_perm, k_perm=k_perm, v_perm=v_perm,
                       ext_map=ext_map, ext_q_sizes=ext_q, ext_k_sizes=ext_k, indices=indices, out_perm=out_perm)
     return output
+
+
+def processor_prologue(attn, hidden_states, encoder_hidden_states, image_rotary_emb, rotary):
+    """q, k, v [B,H,S,D] that PecoAttention.__call__ hands to attention (peco/processor.py:163-187).
+
+    Single-stream blocks (no add_q_proj) project [video, text] with the same weights and
+    rotate only the video rows; double-stream blocks project the text with the added
+    projections and norms. ``rotary(x, freqs)`` is the rotary function.
+    """
+    text_length = 0 if encoder_hidden_states is None else encoder_hidden_states.shape[1]
+    if attn.add_q_proj is None and text_length:
+        hidden_states = torch.cat((hidden_states, encoder_hidden_states), 1)
+
+    def split_heads(x):
+        return x.unflatten(2, (attn.heads, -1)).transpose(1, 2)
+
+    query, key, value = (split_heads(proj(hidden_states)) for proj in (attn.to_q, attn.to_k, attn.to_v))
+    if attn.norm_q is not None:
+        query = attn.norm_q(query)
+    if attn.norm_k is not None:
+        key = attn.norm_k(key)
+    if image_rotary_emb is not None:
+        if attn.add_q_proj is None and text_length:
+            query = torch.cat((rotary(query[:, :, :-text_length], image_rotary_emb), query[:, :, -text_length:]), 2)
+            key = torch.cat((rotary(key[:, :, :-text_length], image_rotary_emb), key[:, :, -text_length:]), 2)
+        else:
+            query, key = (rotary(x, image_rotary_emb) for x in (query, key))
+    if attn.add_q_proj is not None and text_length:
+        eq, ek, ev = (split_heads(proj(encoder_hidden_states))
+                      for proj in (attn.add_q_proj, attn.add_k_proj, attn.add_v_proj))
+        if attn.norm_added_q is not None:
+            eq = attn.norm_added_q(eq)
+        if attn.norm_added_k is not None:
+            ek = attn.norm_added_k(ek)
+        query, key, value = torch.cat((query, eq), 2), torch.cat((key, ek), 2), torch.cat((value, ev), 2)
+    return query.contiguous(), key.contiguous(), value.contiguous()
+
+
+def processor_epilogue(attn, output, encoder_hidden_states):
+    """(video output, text output) of PecoAttention.__call__ from the attention output
+    [B,H,S,D] (peco/processor.py:188-197): no output projections when there is no text."""
+    text_length = 0 if encoder_hidden_states is None else encoder_hidden_states.shape[1]
+    output = output.transpose(1, 2).flatten(2, 3)
+    if not text_length:
+        return output, encoder_hidden_states
+    output, encoder_output = output[:, :-text_length], output[:, -text_length:]
+    if getattr(attn, "to_out", None) is not None:
+        output = attn.to_out[1](attn.to_out[0](output))
+    if getattr(attn, "to_add_out", None) is not None:
+        encoder_output = attn.to_add_out(encoder_output)
+    return output, encoder_output
+
+
+def rotary_embedding(x, freqs_cis):
+    """diffusers' apply_rotary_emb(x, (cos, sin), use_real=True, use_real_unbind_dim=-1):
+    channel pairs (2i, 2i+1) rotated by the tables [S, D] (HunyuanVideo's call)."""
+    cos, sin = freqs_cis
+    cos, sin = cos[None, None], sin[None, None]
+    real, imag = x.reshape(*x.shape[:-1], -1, 2).unbind(-1)
+    rotated = torch.stack([-imag, real], dim=-1).flatten(3)
+    return (x.float() * cos + rotated.float() * sin).to(x.dtype)

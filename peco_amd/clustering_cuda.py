@@ -120,6 +120,9 @@ class KMeansProblem:
     def __init__(self, x, init_centers):
         if x.ndim != 3 or x.stride(2) != 1 or x.stride(1) != x.shape[2]:
             raise ValueError("x must be [B,N,D] with contiguous token rows")
+        if init_centers.ndim != 3 or init_centers.shape[0] != x.shape[0] or init_centers.shape[2] != x.shape[2] \
+                or not 1 <= init_centers.shape[1] <= x.shape[1] or init_centers.device != x.device:
+            raise ValueError("init_centroids must match [batch_heads, n_clusters, dims] and x.device")
         self.x = x
         self.init = init_centers.float().contiguous()
         self.batch, self.tokens, self.dims = x.shape

@@ -448,8 +448,12 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     constexpr int NB = D / 32;      // 32-channel blocks of O^T
     // Scores may run up to 2^8 above the running maximum before O is rescaled.
     constexpr float kLazyLog2 = 8.0f;
-    __shared__ __align__(16) uint16_t ks[2][T::kElems];
-    __shared__ __align__(16) uint16_t vs[2][T::kElems];
+    // K tiles (buffers 0, 1) and V tiles (2, 3) in one array: after the last tile the paired
+    // waves exchange their softmax states through it, which takes more than the K half.
+    __shared__ __align__(16) uint16_t kvs[4][T::kElems];
+    uint16_t(*const ks)[T::kElems] = kvs;
+    uint16_t(*const vs)[T::kElems] = kvs + 2;
+    static_assert(2 * kWave * (NB * 16 + 2) * sizeof(float) <= sizeof(kvs), "pair exchange exceeds the tile LDS");
     __shared__ int prow[2][kKTile];
     __shared__ int pidx[2][kKTile];    // k_index values of tile t+3 rows (indexed inputs)
     __shared__ int tmp[4];
@@ -742,9 +746,10 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last index load
     if (split) {
         // Merge the pair's states: the second-half wave (hb = 1) leaves m, l and O in the tile
-        // LDS (free after the loop's last barrier), the first-half wave rescales both to the
-        // larger maximum and adds. Lane l of both waves holds the same query rows.
-        float* xch = reinterpret_cast<float*>(&ks[0][0]) + (rb * kWave + lane) * (NB * 16 + 2);
+        // LDS (the K and V buffers, free after the loop's last barrier), the first-half wave
+        // rescales both to the larger maximum and adds. Lane l of both waves holds the same
+        // query rows.
+        float* xch = reinterpret_cast<float*>(&kvs[0][0]) + (rb * kWave + lane) * (NB * 16 + 2);
         if (hb == 1 && wave_active) {
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)
@@ -917,3 +922,4 @@ PECO_API int peco_sparse_attention(const void* q, const void* k, const void* v, 
     return peco_sparse_attention_ex(q, k, v, selected, q_sizes, k_sizes, output, nullptr, 0, nullptr, workspace,
                                     ref_ints, bh, sq, sk, d, cq, ck, dtype, stream);
 }
+

@@ -121,7 +121,8 @@ __device__ __forceinline__ void split_neg2(float c, uint16_t& hi, uint16_t& lo) 
     lo = f32_to_bf16_bits(v - bf16_bits_to_f32(hi));
 }
 
-// Initial preparation: norms + split of the initial centres; clears the tile histograms.
+// Initial preparation: norms + split of the initial centres (when the problem has split
+// buffers); clears the tile histograms.
 template <int D>
 __global__ __launch_bounds__(64) void km_prep_kernel(KmArgs a, KmIter it) {
     __shared__ float row[D];
@@ -134,10 +135,12 @@ __global__ __launch_bounds__(64) void km_prep_kernel(KmArgs a, KmIter it) {
     for (int d = threadIdx.x; d < D; d += kWave) {
         const float v = c[d];
         row[d] = v;
-        uint16_t hi, lo;
-        split_neg2(v, hi, lo);
-        P.prep_hi[static_cast<int64_t>(local) * D + d] = hi;
-        P.prep_lo[static_cast<int64_t>(local) * D + d] = lo;
+        if (P.prep_hi) {
+            uint16_t hi, lo;
+            split_neg2(v, hi, lo);
+            P.prep_hi[static_cast<int64_t>(local) * D + d] = hi;
+            P.prep_lo[static_cast<int64_t>(local) * D + d] = lo;
+        }
     }
     __syncthreads();
     if (threadIdx.x == 0) P.norms[local] = canonical_norm_lds(row, D);
@@ -226,17 +229,35 @@ template <int D> struct CentreRegs {
     float norm;
 };
 
-template <int D>
+// kRaw: the split planes are made here from the fp32 centres (raw), so a caller needs no
+// buffer for them; otherwise they are read from hi_base/lo_base.
+template <int D, bool kRaw>
 __device__ __forceinline__ void load_centres(CentreRegs<D>& R, const uint16_t* hi_base, const uint16_t* lo_base,
-                                             const float* norms, int cb, int K, int tid) {
+                                             const float* raw, const float* norms, int cb, int K, int tid) {
     using T = AssignTiles<D>;
 #pragma unroll
     for (int i = 0; i < T::kLoads; ++i) {
         const int id = i * kAssignThreads + tid;
         const int row = min(cb + id / T::kChunks, K - 1);  // rows past K are never selected
         const int64_t e = static_cast<int64_t>(row) * D + (id % T::kChunks) * 8;
-        R.hi[i] = *reinterpret_cast<const u32x4*>(hi_base + e);
-        R.lo[i] = *reinterpret_cast<const u32x4*>(lo_base + e);
+        if constexpr (kRaw) {
+            const f32x4 a = *reinterpret_cast<const f32x4*>(raw + e);
+            const f32x4 b = *reinterpret_cast<const f32x4*>(raw + e + 4);
+            uint16_t h[8], l[8];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                split_neg2(a[k], h[k], l[k]);
+                split_neg2(b[k], h[4 + k], l[4 + k]);
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                R.hi[i][k] = static_cast<uint32_t>(h[2 * k]) | (static_cast<uint32_t>(h[2 * k + 1]) << 16);
+                R.lo[i][k] = static_cast<uint32_t>(l[2 * k]) | (static_cast<uint32_t>(l[2 * k + 1]) << 16);
+            }
+        } else {
+            R.hi[i] = *reinterpret_cast<const u32x4*>(hi_base + e);
+            R.lo[i] = *reinterpret_cast<const u32x4*>(lo_base + e);
+        }
     }
     if (tid < 32) R.norm = cb + tid < K ? norms[cb + tid] : kFarAway;
 }
@@ -290,7 +311,9 @@ __device__ __forceinline__ float canonical_dot(const void* x, int64_t xrow, cons
     return dot;
 }
 
-template <int DT, int D>
+// kRaw: centre blocks are split from the fp32 centres it.src as they are loaded (the
+// reference-ABI assignment, which has no buffer for the split planes).
+template <int DT, int D, bool kRaw = false>
 __global__ __launch_bounds__(kAssignThreads, 2) void km_assign_kernel(KmArgs a, KmIter it) {
     using T = AssignTiles<D>;
     constexpr int S = D / 16;                 // MFMA k-steps over channels
@@ -313,9 +336,10 @@ __global__ __launch_bounds__(kAssignThreads, 2) void km_assign_kernel(KmArgs a, 
     const float* norms = P.norms + static_cast<int64_t>(b) * K;
     const uint16_t* hi_base = P.prep_hi + static_cast<int64_t>(b) * K * D;
     const uint16_t* lo_base = P.prep_lo + static_cast<int64_t>(b) * K * D;
+    const float* raw_base = it.src[p] + static_cast<int64_t>(b) * K * D;
 
     CentreRegs<D> regs;
-    load_centres<D>(regs, hi_base, lo_base, norms, 0, K, tid);
+    load_centres<D, kRaw>(regs, hi_base, lo_base, raw_base, norms, 0, K, tid);
     const float n0 = norms[min(tid, K - 1)];
     float nmax = tid < K ? n0 : 0.0f;
 
@@ -431,7 +455,7 @@ __global__ __launch_bounds__(kAssignThreads, 2) void km_assign_kernel(KmArgs a, 
     // share of the tracking) and execute overlapped within the wavefront.
     auto step = [&](int blk, const f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
         const bool has2 = blk + 2 < nblocks;
-        if (has2) load_centres<D>(regs, hi_base, lo_base, norms, (blk + 2) * 32, K, tid);
+        if (has2) load_centres<D, kRaw>(regs, hi_base, lo_base, raw_base, norms, (blk + 2) * 32, K, tid);
         screen((blk + 1) & 1, nxt);
         track(blk, cur);
         // Per channel step s its MFMAs, each followed by a share of the tracking; the centre
@@ -463,7 +487,7 @@ __global__ __launch_bounds__(kAssignThreads, 2) void km_assign_kernel(KmArgs a, 
     f32x16 acc_a[2];
     if constexpr (kPipelined) {
         f32x16 acc_b[2];
-        if (nblocks > 1) load_centres<D>(regs, hi_base, lo_base, norms, 32, K, tid);
+        if (nblocks > 1) load_centres<D, kRaw>(regs, hi_base, lo_base, raw_base, norms, 32, K, tid);
         screen(0, acc_a);
         if (nblocks > 1) {
             store_centres<D>(regs, chi[1], clo[1], cn[1], tid);
@@ -483,7 +507,7 @@ __global__ __launch_bounds__(kAssignThreads, 2) void km_assign_kernel(KmArgs a, 
     } else {
         for (int blk = 0; blk < nblocks; ++blk) {
             const bool more = blk + 1 < nblocks;
-            if (more) load_centres<D>(regs, hi_base, lo_base, norms, (blk + 1) * 32, K, tid);
+            if (more) load_centres<D, kRaw>(regs, hi_base, lo_base, raw_base, norms, (blk + 1) * 32, K, tid);
             screen(blk & 1, acc_a);
             track(blk, acc_a);
             if (more) store_centres<D>(regs, chi[(blk + 1) & 1], clo[(blk + 1) & 1], cn[(blk + 1) & 1], tid);
@@ -1077,32 +1101,27 @@ PECO_API int peco_kmeans_fit(int num_problems, const void* const* x, const int64
 }
 
 // Reference ABI (peco/kernels/kmeans.cu:139): one assignment of fp32 x [B,N,D] to centres
-// [B,C,D]. scratch/chunk_size are accepted for ABI compatibility and unused; center_norms
-// receives the canonical norms. Internal buffers come from the stream-ordered allocator.
+// [B,C,D]. center_norms receives the canonical norms (when null, the first B*C floats of
+// scratch hold them; the reference always passes both). chunk_size is accepted for ABI
+// compatibility and unused. Nothing is allocated: the split-bf16 centre planes are made
+// inside the assign kernel as its centre blocks are loaded.
 PECO_API int peco_assign_tokens_to_centers(const float* x, const float* centers, int32_t* labels, float* scratch,
                                            float* center_norms, int batch, int tokens, int dims, int clusters,
                                            int chunk_size, void* stream) {
-    (void)scratch;
     (void)chunk_size;
-    if (!x || !centers || !labels || batch < 1 || tokens < 1 || clusters < 1 || (dims != 64 && dims != 128))
+    float* norms = center_norms ? center_norms : scratch;
+    if (!x || !centers || !labels || !norms || batch < 1 || tokens < 1 || clusters < 1 ||
+        (dims != 64 && dims != 128))
         return kInvalidValue;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     KmArgs a{};
     a.num = 1;
     KmProblem& P = a.p[0];
-    const size_t bkd = static_cast<size_t>(batch) * clusters * dims;
-    void* buf = nullptr;
-    const size_t bytes = bkd * 4 + (center_norms ? 0 : static_cast<size_t>(batch) * clusters * 4) + 256;
-    hipError_t e = hipMallocAsync(&buf, bytes, s);
-    if (e != hipSuccess) return e;
-    char* w = static_cast<char*>(buf);
     P.x = x;
     P.x_stride = static_cast<int64_t>(tokens) * dims;
-    P.prep_hi = reinterpret_cast<uint16_t*>(w);
-    P.prep_lo = P.prep_hi + bkd;
-    w += bkd * 4;
-    if (center_norms) P.norms = center_norms;
-    else { P.norms = reinterpret_cast<float*>(w); w += static_cast<size_t>(batch) * clusters * 4; }
+    P.prep_hi = nullptr;
+    P.prep_lo = nullptr;
+    P.norms = norms;
     P.labels = labels;
     P.batch = batch;
     P.tokens = tokens;
@@ -1117,14 +1136,14 @@ PECO_API int peco_assign_tokens_to_centers(const float* x, const float* centers,
     it.src[0] = centers;
     if (dims == 128) {
         hipLaunchKernelGGL((km_prep_kernel<128>), dim3(a.total_update_blocks), dim3(64), 0, s, a, it);
-        hipLaunchKernelGGL((km_assign_kernel<kF32, 128>), dim3(a.total_assign_blocks), dim3(kAssignThreads), 0, s, a, it);
+        hipLaunchKernelGGL((km_assign_kernel<kF32, 128, true>), dim3(a.total_assign_blocks), dim3(kAssignThreads), 0,
+                           s, a, it);
     } else {
         hipLaunchKernelGGL((km_prep_kernel<64>), dim3(a.total_update_blocks), dim3(64), 0, s, a, it);
-        hipLaunchKernelGGL((km_assign_kernel<kF32, 64>), dim3(a.total_assign_blocks), dim3(kAssignThreads), 0, s, a, it);
+        hipLaunchKernelGGL((km_assign_kernel<kF32, 64, true>), dim3(a.total_assign_blocks), dim3(kAssignThreads), 0,
+                           s, a, it);
     }
-    e = hipGetLastError();
-    hipError_t f = hipFreeAsync(buf, s);
-    return e != hipSuccess ? e : f;
+    return hipGetLastError();
 }
 
 // Reference ABI (peco/kernels/kmeans.cu:179): means/counts of fp32 x [B,N,D] for labels

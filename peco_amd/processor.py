@@ -107,6 +107,15 @@ def _extend_partition_on_device(dynamic_map, q_sizes, k_sizes, valid_text, text_
             torch.cat((k_sizes.to(torch.int32), extra), -1).contiguous())
 
 
+def _rotary_function():
+    """diffusers' apply_rotary_emb when diffusers is installed, else the restatement below."""
+    try:
+        from diffusers.models.embeddings import apply_rotary_emb
+    except ImportError:
+        return _apply_rotary_emb
+    return apply_rotary_emb
+
+
 def _apply_rotary_emb(x, freqs_cis):
     """Rotary embedding with (cos, sin) tables [S, D] over interleaved channel pairs.
 
@@ -164,6 +173,10 @@ class PecoAttention:
     @staticmethod
     def _initial_centers(x, cached, clusters):
         if cached is not None:
+            # A cache from a call with other heads, dims or device must not reach the kernels,
+            # which size every centre buffer from x (peco/clustering.py:51-52).
+            if tuple(cached.shape) != (x.shape[0], clusters, x.shape[2]) or cached.device != x.device:
+                raise ValueError("init_centroids must match [batch_heads, n_clusters, dims] and x.device")
             return cached
         tokens = x.shape[1]
         if not 1 <= clusters <= tokens:
@@ -215,47 +228,52 @@ class PecoAttention:
 
     @torch.no_grad()
     def __call__(self, attn, hidden_states, encoder_hidden_states=None, attention_mask=None, image_rotary_emb=None):
-        """diffusers attention-processor entry (peco/processor.py:159-197)."""
-        try:
-            from diffusers.models.embeddings import apply_rotary_emb
-        except ImportError:
-            apply_rotary_emb = _apply_rotary_emb
+        """diffusers attention-processor entry (peco/processor.py:159-197).
 
-        text_length = 0 if encoder_hidden_states is None else encoder_hidden_states.shape[1]
-        if attn.add_q_proj is None and text_length:
-            hidden_states = torch.cat((hidden_states, encoder_hidden_states), 1)
-
-        def split_heads(x):
-            return x.unflatten(2, (attn.heads, -1)).transpose(1, 2)
-
-        query, key, value = (split_heads(proj(hidden_states)) for proj in (attn.to_q, attn.to_k, attn.to_v))
-        if attn.norm_q is not None:
-            query = attn.norm_q(query)
-        if attn.norm_k is not None:
-            key = attn.norm_k(key)
-        if image_rotary_emb is not None:
-            if attn.add_q_proj is None and text_length:
-                query = torch.cat((apply_rotary_emb(query[:, :, :-text_length], image_rotary_emb),
-                                   query[:, :, -text_length:]), 2)
-                key = torch.cat((apply_rotary_emb(key[:, :, :-text_length], image_rotary_emb),
-                                 key[:, :, -text_length:]), 2)
+        ``attention_mask`` is ignored: which text rows are valid comes from the shared
+        InferenceContext. The sequence is [video rows, text rows]. Each projection of each
+        part is written once, head-major, into its slot of one [3, B, H, S, D] buffer (the
+        copy that splits the heads also places the rows), so no concatenation copies are
+        made. Video rows get the rotary embedding; text rows never do. Double-stream blocks
+        (``add_q_proj`` set) project the text with their added projections and norms,
+        single-stream blocks with the same ones as the video.
+        """
+        rotary = _rotary_function()
+        text = 0 if encoder_hidden_states is None else encoder_hidden_states.shape[1]
+        parts = [(hidden_states, (attn.to_q, attn.to_k, attn.to_v), (attn.norm_q, attn.norm_k),
+                  image_rotary_emb)]
+        if text:
+            if attn.add_q_proj is not None:
+                parts.append((encoder_hidden_states, (attn.add_q_proj, attn.add_k_proj, attn.add_v_proj),
+                              (attn.norm_added_q, attn.norm_added_k), None))
             else:
-                query, key = (apply_rotary_emb(x, image_rotary_emb) for x in (query, key))
-        if attn.add_q_proj is not None and text_length:
-            eq, ek, ev = (split_heads(proj(encoder_hidden_states))
-                          for proj in (attn.add_q_proj, attn.add_k_proj, attn.add_v_proj))
-            if attn.norm_added_q is not None:
-                eq = attn.norm_added_q(eq)
-            if attn.norm_added_k is not None:
-                ek = attn.norm_added_k(ek)
-            query, key, value = torch.cat((query, eq), 2), torch.cat((key, ek), 2), torch.cat((value, ev), 2)
-        output = self.attention(query.contiguous(), key.contiguous(), value.contiguous())
-        output = output.transpose(1, 2).flatten(2, 3).to(query.dtype)
-        if not text_length:
-            return output, encoder_hidden_states
-        output, encoder_output = output[:, :-text_length], output[:, -text_length:]
+                parts.append((encoder_hidden_states, (attn.to_q, attn.to_k, attn.to_v), (attn.norm_q, attn.norm_k),
+                              None))
+        length = hidden_states.shape[1] + text
+        qkv = None
+        first = 0
+        for source, projections, norms, freqs in parts:
+            rows = source.shape[1]
+            for slot, proj in enumerate(projections):
+                part = proj(source).unflatten(2, (attn.heads, -1)).transpose(1, 2)  # [B, H, rows, D] view
+                if slot < 2:
+                    if norms[slot] is not None:
+                        part = norms[slot](part)
+                    if freqs is not None:
+                        part = rotary(part, freqs)
+                if qkv is None:
+                    batch, heads, _, dim = part.shape
+                    qkv = torch.empty((3, batch, heads, length, dim), dtype=part.dtype, device=part.device)
+                qkv[slot, :, :, first:first + rows] = part
+            first += rows
+        output = self.attention(qkv[0], qkv[1], qkv[2]).transpose(1, 2)  # [B, S, H, D] view
+        video = hidden_states.shape[1]
+        if not text:
+            return output.flatten(2, 3), encoder_hidden_states
+        video_out = output[:, :video].flatten(2, 3)
+        text_out = output[:, video:].flatten(2, 3)
         if getattr(attn, "to_out", None) is not None:
-            output = attn.to_out[1](attn.to_out[0](output))
+            video_out = attn.to_out[1](attn.to_out[0](video_out))
         if getattr(attn, "to_add_out", None) is not None:
-            encoder_output = attn.to_add_out(encoder_output)
-        return output, encoder_output
+            text_out = attn.to_add_out(text_out)
+        return video_out, text_out

@@ -165,6 +165,16 @@ def test_install_attention_and_reset_state():
     assert (ctx.step, ctx.text_length, ctx.valid_text_length) == (0, 4, 3)
     with pytest.raises(ValueError, match="right padding"):
         pipe.transformer(torch.zeros(1), encoder_attention_mask=torch.tensor([[1, 0, 1, 0]]))
-    pipe.transformer._peco_processors[0].q_centroids = torch.zeros(1)
+    processors = pipe.transformer._peco_installation.processors
+    assert [p.layer_idx for p in processors] == [0, 1, 2]
+    processors[0].q_centroids = torch.zeros(1)
     model.reset_state(pipe)
-    assert ctx.step == -1 and pipe.transformer._peco_processors[0].q_centroids is None
+    assert ctx.step == -1 and processors[0].q_centroids is None
+    # Installing again replaces the hook: one transformer call advances the new context once,
+    # and the old context no more.
+    ctx2 = model.install_attention(pipe, processor.PecoConfig())
+    pipe.transformer(torch.zeros(1), encoder_attention_mask=torch.tensor([[1, 1, 0, 0]]))
+    assert (ctx2.step, ctx2.text_length, ctx2.valid_text_length) == (0, 4, 2)
+    assert ctx.step == -1
+    with pytest.raises(ValueError, match="one prompt"):
+        pipe.transformer(torch.zeros(1), encoder_attention_mask=torch.ones(2, 4))

@@ -74,6 +74,11 @@ def test_layer_matches_oracle(announce, name, heads, video):
     rl, rc, _, ridx, _ = canonical.kmeans_fit(xq, wl.q_init.numpy(), iters)
     assert np.array_equal(q_idx.cpu().numpy(), ridx)
     assert np.array_equal(layer.q_centroids.cpu().numpy().view(np.int32), rc.view(np.int32))
+    # K has the larger cluster count, where the saturated-list fallback of the assign runs.
+    xk = wl.key[0, :, :n].float().numpy()
+    _, kc, _, kidx, _ = canonical.kmeans_fit(xk, wl.k_init.numpy(), iters)
+    assert np.array_equal(k_idx.cpu().numpy(), kidx)
+    assert np.array_equal(layer.k_centroids.cpu().numpy().view(np.int32), kc.view(np.int32))
     # The torch-literal k-means of the reference path agrees with the canonical labels
     # except at near-ties (its bmm summation order is MKL's).
     tl, _, _, _ = reference_path.fit_token_clusters(torch.from_numpy(xq), wl.shape.num_q_centroids, iters, wl.q_init)
@@ -197,3 +202,39 @@ def test_layer_head_bands_bit_exact(announce):
     _, out2 = _run_layer(part, iters)
     assert torch.isfinite(out.float()).all()
     assert torch.equal(out[:, :2], out2)
+
+
+def test_layer_full_length_720p_head_matches_oracle(announce):
+    """One head of the 720p layer at its full length (118800 video + 256 text tokens, 256/1024
+    clusters, 8 iterations, 15% of key clusters kept, Base-Offset 4-bit). Permutations and
+    centroids of Q and K are bit-exact against the C oracle's fit; the output is compared with
+    the oracle's layer, whose block-sparse attention runs in fp32 torch on the CPU (the
+    float64 brute force would take minutes at this length)."""
+    wl = workloads.make_workload("hunyuan_720p", heads=1)
+    shape = wl.shape
+    iters = shape.iterations
+    n = shape.video
+    announce(f"hunyuan_720p full length: heads=1 video={n} clusters={shape.num_q_centroids}/"
+             f"{shape.num_k_centroids} iters={iters} bits={shape.bits}")
+    layer, out = _run_layer(wl, iters)
+    q_idx, k_idx = (t.cpu().numpy() for t in layer._last_fit)
+    fits = {}
+    for name, x, init in (("q", wl.query, wl.q_init), ("k", wl.key, wl.k_init)):
+        fits[name] = canonical.kmeans_fit(x[0, :, :n].float().numpy(), init.numpy(), iters)
+    assert np.array_equal(q_idx, fits["q"][3]), "Q permutation"
+    assert np.array_equal(k_idx, fits["k"][3]), "K permutation"
+    assert np.array_equal(layer.q_centroids.cpu().numpy().view(np.int32), fits["q"][1].view(np.int32))
+    assert np.array_equal(layer.k_centroids.cpu().numpy().view(np.int32), fits["k"][1].view(np.int32))
+
+    def fit(x, clusters, iterations, init):
+        labels, centers, counts, _, _ = fits["q" if clusters == shape.num_q_centroids else "k"]
+        return torch.from_numpy(labels), torch.from_numpy(centers), torch.from_numpy(counts), iterations
+
+    ref = reference_path.peco_layer(
+        wl.query, wl.key, wl.value, num_q_centroids=shape.num_q_centroids, num_k_centroids=shape.num_k_centroids,
+        iterations=iters, q_init=wl.q_init, k_init=wl.k_init, top_p=wl.top_p, min_kc_ratio=wl.min_kc_ratio,
+        bits=shape.bits, text_length=shape.text, valid_text=shape.text, fit=fit)
+    err = (out.float().cpu() - ref.float()).abs()
+    print(f"[720p head] max {err.max().item():.3e} mean {err.mean().item():.3e}", flush=True)
+    assert err.mean().item() <= 2e-3
+    assert err.max().item() <= 2e-2

@@ -435,3 +435,44 @@ def test_select_with_text_partition_matches_oracle(announce):
     # Kept key rows of every (extended) map row: the sizes of its kept columns.
     ref_kept = (rm.to(torch.int64) * rk[:, :, None, :].to(torch.int64)).sum(-1).to(torch.int32)
     assert torch.equal(kept.cpu(), ref_kept)
+
+
+def _threshold_case(m, rows=4, ck=64, dims=128, seed=0):
+    """Centroids whose count-weighted probabilities are exactly fl(1/m) for m keys of each
+    row and 0 for the others: integer entries make every score exact in any summation order,
+    unit counts make the log-count term 0, and the other keys score 226 lower, so their exp
+    is exactly 0. Each row is its own head (one query cluster, ck key clusters), with its m
+    keys at random positions."""
+    g = _gen(seed)
+    kc = torch.zeros(1, rows, ck, dims)
+    for r in range(rows):
+        kc[0, r, torch.randperm(ck, generator=g)[:m]] = 20.0
+    qc = torch.ones(1, rows, 1, dims)
+    qs = torch.ones(1, rows, 1, dtype=torch.int32)
+    ks = torch.ones(1, rows, ck, dtype=torch.int32)
+    return qc, kc, qs, ks
+
+
+@pytest.mark.parametrize("m", [3, 7, 10, 20])
+def test_select_near_threshold_matches_oracle(announce, m):
+    """Keep decisions where a prefix sum lands within an ulp of top_p. The selection follows
+    torch's CPU semantics (the oracle): cumsum accumulated in double and rounded per element,
+    `before` = fl(cumsum) - prob in fp32, compared against fp32(top_p). Thresholds are the
+    default 0.9, every `before` value of the row, and their fp32 neighbours."""
+    qc, kc, qs, ks = _threshold_case(m, seed=m)
+    prob = np.float32(1.0) / np.float32(m)
+    befores = (np.cumsum(np.full(m, prob, np.float64)).astype(np.float32) - prob).astype(np.float32)
+    ps = {0.9}
+    for b in befores[1:]:
+        for v in (b, np.nextafter(b, np.float32(1)), np.nextafter(b, np.float32(0))):
+            if 0 < v <= 1:
+                ps.add(float(v))
+    announce(f"m={m} thresholds={len(ps)}")
+    kept_counts = set()
+    for p in sorted(ps):
+        got = clustering.select_cluster_connections(qc.to(DEV), kc.to(DEV), qs.to(DEV), ks.to(DEV), p, 0.0).cpu()
+        ref = reference_path.select_connections(qc, kc, qs, ks, p, 0.0)
+        assert torch.equal(got, ref), f"p={p!r}"
+        kept_counts.add(int(ref[0, 0, 0].sum()))
+    # The thresholds straddle every crossing: each prefix length 1..m occurs.
+    assert kept_counts == set(range(1, m + 1))
