@@ -143,6 +143,16 @@ int peco_select_cluster_connections(const float* qc, const float* kc, const int3
                                     int extend, int valid_text, int text, uint8_t* map, int32_t* ext_q,
                                     int32_t* ext_k, int32_t* kept_keys, void* stream);
 
+/* peco_sparse_attention without a workspace argument. No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph capture, serving loops
+ * that forbid hipMalloc). The work list lives in a static per-device array of 1048576 int32
+ * (4 MiB per GPU, held until the process ends); a problem whose work list
+ * (peco_sparse_attention_workspace_size) is larger returns 20004. Calls that overlap on one
+ * GPU share that array and race; calls ordered on one stream do not. Allocates nothing. */
+int peco_sparse_attention_noalloc(const void* q, const void* k, const void* v, const uint8_t* selected,
+                                  const int* q_sizes, const int* k_sizes, void* output, int bh, int sq, int sk,
+                                  int d, int cq, int ck, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -123,6 +123,7 @@ SIGNATURES = {
     "peco_sparse_attention_ex": (I, [P] * 8 + [I, P, P, Z] + [I] * 7 + [P]),
     "peco_sparse_attention_indexed": (I, [P] * 9 + [I, P, P, Z] + [I] * 7 + [P]),
     "peco_select_cluster_connections": (I, [P] * 4 + [I] * 4 + [ctypes.c_float] + [I] * 4 + [P] * 5),
+    "peco_sparse_attention_noalloc": (I, [P] * 7 + [I] * 7 + [P]),
 }
 
 

@@ -10,6 +10,9 @@ const char* peco_status(int code) {
         case kWorkspaceTooSmall: return "PECO: workspace too small";
         case kUnsupportedShape: return "PECO: unsupported shape (head dim must be 64 or 128; cluster counts within limits)";
         case kUnsupportedDtype: return "PECO: unsupported dtype";
+        case kScratchExceeded:
+            return "PECO: problem exceeds the static scratch of peco_sparse_attention_noalloc "
+                   "(work list of at most 1048576 int32; use peco_sparse_attention with a workspace)";
         default: return hipGetErrorString(static_cast<hipError_t>(code));
     }
 }

@@ -29,6 +29,7 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 namespace peco {
@@ -923,3 +924,54 @@ PECO_API int peco_sparse_attention(const void* q, const void* k, const void* v, 
                                     ref_ints, bh, sq, sk, d, cq, ck, dtype, stream);
 }
 
+// ---- Allocation-free variant (no counterpart in the reference) ----
+//
+// The work list lives in a file-scope device array instead of a caller workspace, for callers
+// that cannot allocate (code under HIP graph capture, serving loops that forbid allocation).
+// Each GPU holds its own copy of the array (4 MiB) until the process ends. Every call on a
+// GPU uses that GPU's copy, so calls that overlap on one GPU (two streams, or two host
+// threads) race; calls on one stream are ordered. The builder writes every entry it later
+// reads, so nothing needs clearing between calls.
+namespace peco {
+namespace {
+
+constexpr size_t kStaticWorkInts = size_t(1) << 20;
+constexpr int kMaxDevices = 64;
+
+static __device__ __align__(256) int32_t scratch[kStaticWorkInts];
+
+std::mutex g_scratch_mutex;
+int32_t* g_scratch[kMaxDevices] = {};
+
+// Device address of the current device's `scratch`, looked up once per device. The host-side
+// name `scratch` is only a stand-in for the symbol and is never passed to a kernel.
+int current_scratch(int32_t** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return kInvalidValue;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_scratch[dev] = static_cast<int32_t*>(ptr);
+    }
+    *out = g_scratch[dev];
+    return kOk;
+}
+
+}  // namespace
+}  // namespace peco
+
+PECO_API int peco_sparse_attention_noalloc(const void* q, const void* k, const void* v, const uint8_t* selected,
+                                           const int* q_sizes, const int* k_sizes, void* output, int bh, int sq,
+                                           int sk, int d, int cq, int ck, int dtype, void* stream) {
+    if (bh < 1 || sq < 0 || cq < 1 || ck < 1) return kInvalidValue;
+    if (peco_sparse_attention_workspace_size(bh, sq, sk, cq, ck) > kStaticWorkInts) return kScratchExceeded;
+    int32_t* work = nullptr;
+    const int e = current_scratch(&work);
+    if (e != kOk) return e;
+    return launch_sparse_attention(q, k, v, selected, q_sizes, k_sizes, output, nullptr, 0, nullptr, nullptr, work,
+                                   kStaticWorkInts, bh, sq, sk, d, cq, ck, dtype, stream);
+}

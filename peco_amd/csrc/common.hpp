@@ -22,6 +22,7 @@ enum Status : int {
     kWorkspaceTooSmall = 20001,
     kUnsupportedShape = 20002,
     kUnsupportedDtype = 20003,
+    kScratchExceeded = 20004,   // larger than the static scratch of an allocation-free entry
 };
 
 enum DType : int { kF16 = 0, kBF16 = 1, kF32 = 2 };
