@@ -311,6 +311,138 @@ __device__ __forceinline__ float canonical_dot(const void* x, int64_t xrow, cons
     return dot;
 }
 
+// A token row in registers, all of its loads issued together (16-bit rows kept raw).
+template <int DT, int D> struct TokenRow {
+    static constexpr int kVecs = DT == kF32 ? D / 4 : D / 8;  // 16-byte vectors per row
+    u32x4 v[kVecs];
+};
+
+template <int DT, int D>
+__device__ __forceinline__ void load_token_row(const void* x, int64_t row, TokenRow<DT, D>& r) {
+    const u32x4* src = reinterpret_cast<const u32x4*>(static_cast<const char*>(x) + row * (DT == kF32 ? 4 : 2));
+#pragma unroll
+    for (int i = 0; i < TokenRow<DT, D>::kVecs; ++i) r.v[i] = src[i];
+}
+
+template <int DT, int D>
+__device__ __forceinline__ float token_value(const TokenRow<DT, D>& r, int d) {
+    if constexpr (DT == kF32) {
+        return __uint_as_float(r.v[d / 4][d % 4]);
+    } else {
+        const uint32_t w = r.v[d / 8][(d % 8) / 2];
+        return half_to_f32<DT == kBF16 ? kBF16 : kF16>(static_cast<uint16_t>(d % 2 ? w >> 16 : w & 0xffffu));
+    }
+}
+
+// Canonical dot of a register-held token row with the fp32 centre row c (the same fma chain
+// over d ascending as canonical_dot). The centre loads of a round (half the row for 16-bit
+// tokens, a quarter for fp32 tokens, whose row takes twice the registers) are all issued
+// before the chain, which keeps the assign kernel within 256 VGPRs.
+template <int DT, int D>
+__device__ __forceinline__ float canonical_dot_row(const TokenRow<DT, D>& r, const float* c) {
+    constexpr int kRound = DT == kF32 ? D / 4 : D / 2;
+    float dot = 0.0f;
+#pragma unroll
+    for (int d0 = 0; d0 < D; d0 += kRound) {
+        f32x4 cv[kRound / 4];
+#pragma unroll
+        for (int i = 0; i < kRound / 4; ++i) cv[i] = reinterpret_cast<const f32x4*>(c + d0)[i];
+#pragma unroll
+        for (int d = 0; d < kRound; ++d) dot = fmaf(token_value<DT, D>(r, d0 + d), cv[d / 4][d % 4], dot);
+    }
+    return dot;
+}
+
+// Certified decision and stores for the 64 tokens of one wavefront (two 32-token column
+// blocks, first token `first`): t holds each lane half's kTop smallest screened values with
+// packed indices. Labels are written for valid tokens; the tile histogram (when given) counts them.
+template <int DT, int D>
+__device__ __forceinline__ void assign_epilogue(const KmArgs& a, const KmIter& it, int p, int b, int first, int lane,
+                                                const float (&t)[2][kTop], const int (&tok)[2],
+                                                const bool (&valid)[2], const float (&sq)[2], float nmax,
+                                                int ibits) {
+    const KmProblem& P = a.p[p];
+    const int K = P.clusters;
+    const int h = lane / 32;
+    const uint32_t imask = (1u << ibits) - 1u;
+    const float* norms = P.norms + static_cast<int64_t>(b) * K;
+    const float cmax = sqrtf(nmax) * 1.001f;
+    const float* cent = it.src[p] + static_cast<int64_t>(b) * K * D;
+    // Index packing perturbs a value by < 2^ibits ulp.
+    const float pack_rel = 1.01f * __uint_as_float((127u - 23u + static_cast<uint32_t>(ibits)) << 23);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        // The two lane halves of a token hold disjoint centres; combine their lists.
+        float pt[kTop];
+#pragma unroll
+        for (int k = 0; k < kTop; ++k) pt[k] = __shfl_xor(t[c][k], 32, kWave);
+        const float best = fminf(t[c][0], pt[0]);
+        const float second = fminf(fmaxf(t[c][0], pt[0]), fminf(t[c][1], pt[1]));
+        int label = static_cast<int>(__float_as_uint(best) & imask);
+        // Certified decision: gap > thr (= 2E) proves `label` is the canonical argmin. E covers
+        // the split-bf16 screen and the canonical fma chain (kappa), the norm inside the MFMA
+        // accumulation (gamma_acc * |c|^2), fp32 rounding and the index packing.
+        const float xnorm = sqrtf(sq[c]) * 1.001f;
+        const float thr = 1.05f * (2.0f * a.kappa * xnorm * cmax + 2.0f * a.gamma_acc * nmax) +
+                          (4.0f * 5.9604645e-8f + pack_rel) * (fabsf(best) + fabsf(second)) + 1e-30f;
+        const bool flagged = valid[c] && !((second - best) > thr);
+        // Every centre that can still be the canonical argmin screens within `bound`. If a
+        // lane half's kTop smallest all fall inside, its list may have missed one (saturated).
+        const float bound = best + thr;
+        const bool saturated = flagged && (t[c][kTop - 1] <= bound || pt[kTop - 1] <= bound);
+        const int64_t trow = static_cast<int64_t>(b) * P.x_stride + static_cast<int64_t>(tok[c]) * D;
+        uint64_t key = ~0ull;
+        if (flagged && !saturated) {
+            TokenRow<DT, D> row;
+            load_token_row<DT, D>(P.x, trow, row);
+#pragma unroll
+            for (int k = 0; k < kTop; ++k) {
+                if (t[c][k] <= bound) {
+                    const int j = static_cast<int>(__float_as_uint(t[c][k]) & imask);
+                    const float dist = fmaf(-2.0f, canonical_dot_row<DT, D>(row, cent + static_cast<int64_t>(j) * D),
+                                            norms[j]);
+                    const uint64_t kj = (static_cast<uint64_t>(orderable(dist)) << 32) | static_cast<uint32_t>(j);
+                    key = kj < key ? kj : key;
+                }
+            }
+        }
+        {
+            const uint64_t other = __shfl_xor(key, 32, kWave);
+            key = other < key ? other : key;
+        }
+        if (flagged && !saturated) label = static_cast<int>(key & 0xffffffffu);
+        // Rare fallback: canonical re-evaluation of a saturated token over all centres, one
+        // token at a time with the whole wavefront (lane i takes centres i, i + 64, ...).
+        uint64_t pending = __ballot(saturated && h == 0);
+        while (pending) {
+            const int src = __builtin_ctzll(pending);  // lane (h == 0) holding the token
+            pending &= pending - 1;
+            const int64_t srow = static_cast<int64_t>(b) * P.x_stride +
+                                 static_cast<int64_t>(first + 32 * c + src) * D;
+            uint64_t full = ~0ull;
+            TokenRow<DT, D> row;
+            load_token_row<DT, D>(P.x, srow, row);
+            for (int j = lane; j < K; j += kWave) {
+                const float dist =
+                    fmaf(-2.0f, canonical_dot_row<DT, D>(row, cent + static_cast<int64_t>(j) * D), norms[j]);
+                const uint64_t kj = (static_cast<uint64_t>(orderable(dist)) << 32) | static_cast<uint32_t>(j);
+                full = kj < full ? kj : full;
+            }
+#pragma unroll
+            for (int m = 1; m < kWave; m <<= 1) {
+                const uint64_t other = __shfl_xor(full, m, kWave);
+                full = other < full ? other : full;
+            }
+            if (lane == src) label = static_cast<int>(full & 0xffffffffu);
+        }
+        if (valid[c] && h == 0) {
+            P.labels[static_cast<int64_t>(b) * P.tokens + tok[c]] = label;
+            if (it.hist[p])
+                atomicAdd(it.hist[p] + (static_cast<int64_t>(b) * P.sort_tiles + tok[c] / kSortTile) * K + label, 1);
+        }
+    }
+}
+
 // kRaw: centre blocks are split from the fp32 centres it.src as they are loaded (the
 // reference-ABI assignment, which has no buffer for the split planes).
 template <int DT, int D, bool kRaw = false>
@@ -515,77 +647,7 @@ __global__ __launch_bounds__(kAssignThreads, 2) void km_assign_kernel(KmArgs a, 
         }
     }
 
-    const float cmax = sqrtf(nmax) * 1.001f;
-    const float* cent = it.src[p] + static_cast<int64_t>(b) * K * D;
-    // Index packing perturbs a value by < 2^ibits ulp.
-    const float pack_rel = 1.01f * __uint_as_float((127u - 23u + static_cast<uint32_t>(ibits)) << 23);
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-        // The two lane halves of a token hold disjoint centres; combine their lists.
-        float pt[kTop];
-#pragma unroll
-        for (int k = 0; k < kTop; ++k) pt[k] = __shfl_xor(t[c][k], 32, kWave);
-        const float best = fminf(t[c][0], pt[0]);
-        const float second = fminf(fmaxf(t[c][0], pt[0]), fminf(t[c][1], pt[1]));
-        int label = static_cast<int>(__float_as_uint(best) & imask);
-        // Certified decision: gap > thr (= 2E) proves `label` is the canonical argmin. E covers
-        // the split-bf16 screen and the canonical fma chain (kappa), the norm inside the MFMA
-        // accumulation (gamma_acc * |c|^2), fp32 rounding and the index packing.
-        const float xnorm = sqrtf(sq[c]) * 1.001f;
-        const float thr = 1.05f * (2.0f * a.kappa * xnorm * cmax + 2.0f * a.gamma_acc * nmax) +
-                          (4.0f * 5.9604645e-8f + pack_rel) * (fabsf(best) + fabsf(second)) + 1e-30f;
-        const bool flagged = valid[c] && !((second - best) > thr);
-        // Every centre that can still be the canonical argmin screens within `bound`. If a
-        // lane half's kTop smallest all fall inside, its list may have missed one (saturated).
-        const float bound = best + thr;
-        const bool saturated = flagged && (t[c][kTop - 1] <= bound || pt[kTop - 1] <= bound);
-        const int64_t trow = static_cast<int64_t>(b) * P.x_stride + static_cast<int64_t>(tok[c]) * D;
-        uint64_t key = ~0ull;
-        if (flagged && !saturated) {
-#pragma unroll
-            for (int k = 0; k < kTop; ++k) {
-                if (t[c][k] <= bound) {
-                    const int j = static_cast<int>(__float_as_uint(t[c][k]) & imask);
-                    const float dist = fmaf(-2.0f, canonical_dot<DT, D>(P.x, trow, cent + static_cast<int64_t>(j) * D),
-                                            norms[j]);
-                    const uint64_t kj = (static_cast<uint64_t>(orderable(dist)) << 32) | static_cast<uint32_t>(j);
-                    key = kj < key ? kj : key;
-                }
-            }
-        }
-        {
-            const uint64_t other = __shfl_xor(key, 32, kWave);
-            key = other < key ? other : key;
-        }
-        if (flagged && !saturated) label = static_cast<int>(key & 0xffffffffu);
-        // Rare fallback: canonical re-evaluation of a saturated token over all centres, one
-        // token at a time with the whole wavefront (lane i takes centres i, i + 64, ...).
-        uint64_t pending = __ballot(saturated && h == 0);
-        while (pending) {
-            const int src = __builtin_ctzll(pending);  // lane (h == 0) holding the token
-            pending &= pending - 1;
-            const int64_t srow = static_cast<int64_t>(b) * P.x_stride +
-                                 static_cast<int64_t>(tile * kAssignTile + wave * 64 + 32 * c + src) * D;
-            uint64_t full = ~0ull;
-            for (int j = lane; j < K; j += kWave) {
-                const float dist =
-                    fmaf(-2.0f, canonical_dot<DT, D>(P.x, srow, cent + static_cast<int64_t>(j) * D), norms[j]);
-                const uint64_t kj = (static_cast<uint64_t>(orderable(dist)) << 32) | static_cast<uint32_t>(j);
-                full = kj < full ? kj : full;
-            }
-#pragma unroll
-            for (int m = 1; m < kWave; m <<= 1) {
-                const uint64_t other = __shfl_xor(full, m, kWave);
-                full = other < full ? other : full;
-            }
-            if (lane == src) label = static_cast<int>(full & 0xffffffffu);
-        }
-        if (valid[c] && h == 0) {
-            P.labels[static_cast<int64_t>(b) * P.tokens + tok[c]] = label;
-            if (it.hist[p])
-                atomicAdd(it.hist[p] + (static_cast<int64_t>(b) * P.sort_tiles + tok[c] / kSortTile) * K + label, 1);
-        }
-    }
+    assign_epilogue<DT, D>(a, it, p, b, tile * kAssignTile + wave * 64, lane, t, tok, valid, sq, nmax, ibits);
 }
 
 // PER consecutive channels of one row as fp32 (one 32-bit load for two 16-bit channels).
