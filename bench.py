@@ -11,6 +11,11 @@ The roofline object reports the attention kernel (the dominant MFMA kernel): its
 algorithmic FLOPs over its average duration measured with events on the launch stream.
 cpu_baseline times the oracle's restatement of the reference CPU torch path on a bounded
 sample of heads of the same workload.
+
+The default run then times the other benchmark configurations under the same clock and
+reports them under "other_workloads": the 480p layer with Base-Offset 4-bit, the 720p layer
+(118800 + 256 tokens, 256/1024 clusters, 8 iterations, 15% kept, Base-Offset 4-bit) and the
+544p Zipf denoising sequence (10 layer calls on drifting Q/K, warm-started k-means).
 """
 from __future__ import annotations
 
@@ -50,6 +55,8 @@ def parse():
     ap.add_argument("--sequence", action="store_true",
                     help="time the workload's denoising sequence: its `steps` layer calls on drifting Q/K, the "
                          "first from the seeded centroids, the rest warm-started from the previous call's centroids")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="skip the other configurations (Base-Offset 480p, 720p, the 544p Zipf sequence)")
     ap.add_argument("--summarize", metavar="CSV", default=None,
                     help="print per-kernel averages of a rocprofv3 counter_collection.csv or kernel_stats.csv")
     return ap.parse_args()
@@ -151,6 +158,17 @@ def measured_traffic(workload):
     return float(m.group(1)) if m else None
 
 
+def cpu_model():
+    """The host CPU's model name (as lscpu reports it)."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(wl, budget_s):
     """Oracle (reference CPU torch path) on whole heads of the workload until the budget is spent."""
     from oracle import reference_path
@@ -174,6 +192,7 @@ def cpu_baseline(wl, budget_s):
         flops += workloads.attention_flops(stages["ext_map"], stages["ext_q_sizes"], stages["ext_k_sizes"], s.dims)
         done += 1
     return {"value": flops / elapsed / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"{done} of {s.heads} heads of {s.name}, full sequence, oracle reference_path "
                       f"(torch CPU, {threads} threads); {elapsed:.2f} s; "
                       f"layer {1e3 * elapsed / done * s.heads:.1f} ms extrapolated to {s.heads} heads"}
@@ -266,7 +285,7 @@ def profile_target(args):
           flush=True)
 
 
-def run_sequence(args):
+def run_sequence(workload, steps, warmup):
     """Multi-step scenario: one repetition = the workload's `steps` calls of one layer on Q/K
     drifting by N(0, drift^2) per step (V fixed), k-means warm-started between calls.
 
@@ -278,7 +297,7 @@ def run_sequence(args):
     from peco_amd import clustering_cuda, processor, workloads
 
     dev = torch.device("cuda:0")
-    wl = workloads.make_workload(args.workload, device=dev)
+    wl = workloads.make_workload(workload, device=dev)
     s = wl.shape
     calls = max(1, s.steps)
     inputs = [wl]
@@ -308,14 +327,14 @@ def run_sequence(args):
         return outs
 
     with torch.no_grad():
-        for _ in range(args.warmup):
+        for _ in range(warmup):
             sequence()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for _ in range(args.steps):
+        for _ in range(steps):
             sequence()
         torch.cuda.synchronize()
-        ms = (time.perf_counter() - t0) * 1e3 / args.steps
+        ms = (time.perf_counter() - t0) * 1e3 / steps
         evs = []
         sequence(evs)
         torch.cuda.synchronize()
@@ -336,8 +355,8 @@ def run_sequence(args):
     total = sum(flops)
     value = total / (ms * 1e-3) / 1e12
     line = {
-        "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps,
+        "warmup": warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": s.name, "heads": s.heads, "video_tokens": s.video, "text_tokens": s.text,
                    "head_dim": s.dims, "q_clusters": s.num_q_centroids, "k_clusters": s.num_k_centroids,
@@ -348,49 +367,34 @@ def run_sequence(args):
                      "warm_call_ms": round(sum(call_ms[1:]) / max(1, calls - 1), 4)},
         "layer_frac_of_peak": round(value / PEAK_BF16_TFLOPS, 4),
     }
-    print(json.dumps(line), flush=True)
+    return line
 
 
-def main():
-    args = parse()
-    if args.summarize:
-        summarize(args.summarize)
-        return
-    if args.profile_target:
-        profile_target(args)
-        return
-    if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are not part of it",
-                          "n_gpus": args.gpus}))
-        sys.exit(2)
-    if args.sequence:
-        run_sequence(args)
-        return
+def measure(name, steps, warmup, stage_reps, attn_reps=20):
+    """One workload's layer: ms per step, stage times, realised F4 and the attention roofline."""
     from peco_amd import workloads
 
     dev = torch.device("cuda:0")
-    wl = workloads.make_workload(args.workload, device=dev)
+    wl = workloads.make_workload(name, device=dev)
     s = wl.shape
     layer = make_layer(wl)
     q, k, v = wl.query, wl.key, wl.value
     q_init, k_init = wl.q_init, wl.k_init
     with torch.no_grad():
-        for _ in range(args.warmup):
+        for _ in range(warmup):
             run_step(layer, wl, q, k, v, q_init, k_init)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for _ in range(args.steps):
+        for _ in range(steps):
             run_step(layer, wl, q, k, v, q_init, k_init)
         torch.cuda.synchronize()
-        ms = (time.perf_counter() - t0) * 1e3 / args.steps
-        stages, flops, attn_args = stage_breakdown(layer, wl, q, k, v, q_init, k_init, args.stage_reps)
-        t_attn = attention_kernel_time(attn_args)
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        stages, flops, attn_args = stage_breakdown(layer, wl, q, k, v, q_init, k_init, stage_reps)
+        t_attn = attention_kernel_time(attn_args, attn_reps)
     value = flops / (ms * 1e-3) / 1e12
     achieved = flops / (t_attn * 1e-3) / 1e12
-    line = {
-        "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+    out = {
+        "value": round(value, 3), "ms_per_step": round(ms, 4), "steps": steps, "warmup": warmup,
         "config": {"workload": s.name, "heads": s.heads, "video_tokens": s.video, "text_tokens": s.text,
                    "head_dim": s.dims, "q_clusters": s.num_q_centroids, "k_clusters": s.num_k_centroids,
                    "kmeans_iterations": s.iterations, "keep_ratio": s.keep_ratio, "base_offset_bits": s.bits},
@@ -406,9 +410,52 @@ def main():
     f1 = 2.0 * s.dims * s.video * (s.num_q_centroids + s.num_k_centroids) * s.heads * s.iterations
     if stages.get("kmeans"):
         t1 = f1 / (stages["kmeans"] * 1e-3) / 1e12
-        line["kmeans_fit"] = {"flops": f1, "tflops": round(t1, 2), "frac_of_peak": round(t1 / PEAK_BF16_TFLOPS, 4)}
+        out["kmeans_fit"] = {"flops": f1, "tflops": round(t1, 2), "frac_of_peak": round(t1 / PEAK_BF16_TFLOPS, 4)}
+    return out, wl
+
+
+# The other benchmark configurations, timed in the default run after the headline one:
+# (workload, steps, warmup, stage reps, attention reps); the denoising sequence separately.
+OTHER_WORKLOADS = (("hunyuan_480p_bo4", 20, 3, 5, 20), ("hunyuan_720p", 3, 1, 2, 5))
+SEQUENCE_WORKLOAD = ("hunyuan_544p_zipf", 2, 1)
+
+
+def main():
+    args = parse()
+    if args.summarize:
+        summarize(args.summarize)
+        return
+    if args.profile_target:
+        profile_target(args)
+        return
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are not part of it",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    if args.sequence:
+        print(json.dumps(run_sequence(args.workload, args.steps, args.warmup)), flush=True)
+        return
+    head, wl = measure(args.workload, args.steps, args.warmup, args.stage_reps)
+    line = {
+        "metric": METRIC, "value": head["value"], "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": head["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+    }
+    line.update({k_: v_ for k_, v_ in head.items() if k_ not in ("value", "ms_per_step", "steps", "warmup")})
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds)
+    del wl
+    if not args.headline_only and args.workload == "hunyuan_480p":
+        others = {}
+        for name, steps, warmup, stage_reps, attn_reps in OTHER_WORKLOADS:
+            others[name], _ = measure(name, steps, warmup, stage_reps, attn_reps)
+            torch.cuda.empty_cache()
+        name, steps, warmup = SEQUENCE_WORKLOAD
+        seq = run_sequence(name, steps, warmup)
+        others[name + "_sequence"] = {k_: v_ for k_, v_ in seq.items() if k_ not in line or k_ in ("value", "steps",
+                                                                                             "warmup", "ms_per_step",
+                                                                                             "config")}
+        line["other_workloads"] = others
     print(json.dumps(line), flush=True)
 
 
