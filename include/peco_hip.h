@@ -84,6 +84,15 @@ int peco_kmeans_fit(int num_problems, const void* const* x, const int64_t* x_bat
                     const int* batch, const int* tokens, const int* clusters, int dims, int dtype, int iterations,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* Diagnostic of the certified assignment (no counterpart in the reference): for bf16 x
+ * [batch, tokens, dims] and fp32 centres, screened[b,t,j] receives the MFMA screen value
+ * |c_j|^2 - 2 x_t.c_j (split-bf16 centres) that the assignment compares, labels the certified
+ * labels, center_norms the canonical norms. peco_kmeans_screen_bound gives the coefficients
+ * kappa (of |x||c|) and gamma (of |c|^2) of the error bound the certification assumes. */
+int peco_kmeans_screen(const void* x, int dtype, const float* centers, float* center_norms, int32_t* labels,
+                       float* screened, int batch, int tokens, int dims, int clusters, void* stream);
+void peco_kmeans_screen_bound(int dims, float* kappa, float* gamma);
+
 /* Base-Offset PE quantizer (peco/quantization.py:97-150), dims in {64, 128}.
  * encode: codes uint8 [batch,tokens,dims] (nullable), low/scale fp32 [batch,tokens] (nullable).
  * decode: x_hat in `dtype` from codes/low/scale. fake_quant: encode+decode in one pass. */

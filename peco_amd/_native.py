@@ -115,6 +115,8 @@ SIGNATURES = {
     "peco_cluster_sort": (I, [P, I, I, I, P, P, P, P, P, Z, P]),
     "peco_kmeans_workspace_size": (Z, [I, I, I, I]),
     "peco_kmeans_fit": (I, [I, PP, P, PP, PP, PP, PP, PP, PP, IP, IP, IP, I, I, I, P, Z, P]),
+    "peco_kmeans_screen": (I, [P, I, P, P, P, P, I, I, I, I, P]),
+    "peco_kmeans_screen_bound": (None, [I, P, P]),
     "peco_base_offset_encode": (I, [P, I, P, P, I, I, I, I, I, P, P, P, P]),
     "peco_base_offset_decode": (I, [P, P, P, P, P, I, I, I, I, I, P, P]),
     "peco_base_offset_fake_quant": (I, [P, I, P, P, I, I, I, I, I, P, P]),

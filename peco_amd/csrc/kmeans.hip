@@ -82,6 +82,7 @@ struct KmIter {
     const float* src[kMaxKm];  // centres used by this iteration
     float* dst[kMaxKm];        // means written by this iteration
     int32_t* hist[kMaxKm];     // nullable: tile histograms the assign adds its labels to
+    float* screen;             // kDump assignments only: screened distances [batch, tokens, K]
 };
 
 namespace {
@@ -445,7 +446,9 @@ __device__ __forceinline__ void assign_epilogue(const KmArgs& a, const KmIter& i
 
 // kRaw: centre blocks are split from the fp32 centres it.src as they are loaded (the
 // reference-ABI assignment, which has no buffer for the split planes).
-template <int DT, int D, bool kRaw = false>
+// kDump: every screened distance (before the index is packed into it) is also written to
+// it.screen, for measuring the screen's error against its certification bound.
+template <int DT, int D, bool kRaw = false, bool kDump = false>
 __global__ __launch_bounds__(kAssignThreads, 2) void km_assign_kernel(KmArgs a, KmIter it) {
     using T = AssignTiles<D>;
     constexpr int S = D / 16;                 // MFMA k-steps over channels
@@ -572,6 +575,10 @@ __global__ __launch_bounds__(kAssignThreads, 2) void km_assign_kernel(KmArgs a, 
             const uint32_t j = static_cast<uint32_t>(cb + 8 * (i / 4) + 4 * h + (i % 4));
 #pragma unroll
             for (int c = 0; c < 2; ++c) {
+                if constexpr (kDump) {
+                    if (valid[c] && static_cast<int>(j) < K)
+                        it.screen[(static_cast<int64_t>(b) * P.tokens + tok[c]) * K + j] = acc[c][i];
+                }
                 const float v = __uint_as_float((__float_as_uint(acc[c][i]) & ~imask) | j);
 #pragma unroll
                 for (int k = kTop - 1; k > 0; --k) t[c][k] = __builtin_amdgcn_fmed3f(t[c][k - 1], v, t[c][k]);
@@ -1206,6 +1213,56 @@ PECO_API int peco_assign_tokens_to_centers(const float* x, const float* centers,
                            s, a, it);
     }
     return hipGetLastError();
+}
+
+// Diagnostic: the assignment's screened distances. For bf16 x [B,N,D] and fp32 centres
+// [B,C,D], screened[b,t,j] receives the value the MFMA screen of the assign kernel compares
+// (|c_j|^2 - 2 x_t.c_j from split-bf16 centres); center_norms receives the canonical norms and
+// labels the certified labels. Used to measure the screen error against its bound.
+PECO_API int peco_kmeans_screen(const void* x, int dtype, const float* centers, float* center_norms,
+                                int32_t* labels, float* screened, int batch, int tokens, int dims, int clusters,
+                                void* stream) {
+    if (!x || !centers || !center_norms || !labels || !screened || batch < 1 || tokens < 1 || clusters < 1 ||
+        (dims != 64 && dims != 128))
+        return kInvalidValue;
+    if (dtype != kBF16) return kUnsupportedDtype;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    KmArgs a{};
+    a.num = 1;
+    KmProblem& P = a.p[0];
+    P.x = x;
+    P.x_stride = static_cast<int64_t>(tokens) * dims;
+    P.norms = center_norms;
+    P.labels = labels;
+    P.batch = batch;
+    P.tokens = tokens;
+    P.clusters = clusters;
+    P.sort_tiles = sort_tiles(tokens);
+    a.total_assign_blocks = batch * static_cast<int>(ceil_div(tokens, kAssignTile));
+    P.assign_blocks = a.total_assign_blocks;
+    a.total_update_blocks = batch * clusters;
+    a.kappa = km_kappa(kBF16, dims);
+    a.gamma_acc = static_cast<float>(gamma_n(3.0 * dims + 2));
+    KmIter it{};
+    it.src[0] = centers;
+    it.screen = screened;
+    if (dims == 128) {
+        hipLaunchKernelGGL((km_prep_kernel<128>), dim3(a.total_update_blocks), dim3(64), 0, s, a, it);
+        hipLaunchKernelGGL((km_assign_kernel<kBF16, 128, true, true>), dim3(a.total_assign_blocks),
+                           dim3(kAssignThreads), 0, s, a, it);
+    } else {
+        hipLaunchKernelGGL((km_prep_kernel<64>), dim3(a.total_update_blocks), dim3(64), 0, s, a, it);
+        hipLaunchKernelGGL((km_assign_kernel<kBF16, 64, true, true>), dim3(a.total_assign_blocks),
+                           dim3(kAssignThreads), 0, s, a, it);
+    }
+    return hipGetLastError();
+}
+
+// Screen error bound coefficients of the assignment for bf16 tokens: kappa (of |x||c|) and
+// gamma (of |c|^2), as the certified decision uses them.
+PECO_API void peco_kmeans_screen_bound(int dims, float* kappa, float* gamma) {
+    if (kappa) *kappa = km_kappa(kBF16, dims);
+    if (gamma) *gamma = static_cast<float>(gamma_n(3.0 * dims + 2));
 }
 
 // Reference ABI (peco/kernels/kmeans.cu:179): means/counts of fp32 x [B,N,D] for labels

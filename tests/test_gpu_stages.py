@@ -5,12 +5,14 @@ results (labels, permutations, counts, codes) and the fixed-order fp32 results (
 norms, Base-Offset reconstructions) must match bit for bit; attention output must be
 within max-abs 2e-2 and mean-abs 2e-3 of the float64 oracle.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
 
 from oracle import canonical, reference_path
-from peco_amd import attention_cuda, clustering, clustering_cuda, quantization
+from peco_amd import _native, attention_cuda, clustering, clustering_cuda, quantization, workloads
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -476,3 +478,50 @@ def test_select_near_threshold_matches_oracle(announce, m):
         kept_counts.add(int(ref[0, 0, 0].sum()))
     # The thresholds straddle every crossing: each prefix length 1..m occurs.
     assert kept_counts == set(range(1, m + 1))
+
+
+# ---------------------------------------------------------------- the assign screen's error model
+
+@pytest.mark.parametrize("name", ["hunyuan_480p", "hunyuan_720p"])
+def test_assign_screen_error_within_certification_bound(announce, name):
+    """The certified assignment accepts a screened argmin only when its margin exceeds twice
+    an a-priori bound E = kappa |x||c| + gamma |c|^2 on |screened - canonical|, which assumes
+    the MFMA forms exact products and rounds its fp32 accumulation no worse than fp32 adds.
+    AMD does not document gfx950's MFMA accumulation, so this measures the realised screen
+    error against exact float64 distances on the k-means shapes of the 480p and 720p layers
+    (two heads; K and Q with their cluster counts), and requires it to stay below half of
+    kappa |x||c| + gamma |c|^2 (the canonical fp32 chain has its own share of the bound)."""
+    lib = _native.library()
+    wl = workloads.make_workload(name, heads=2, video=8192)
+    n = wl.shape.video
+    kappa, gamma = ctypes.c_float(), ctypes.c_float()
+    lib.peco_kmeans_screen_bound(128, ctypes.byref(kappa), ctypes.byref(gamma))
+    worst = 0.0
+    for label, x, init in (("K", wl.key, wl.k_init), ("Q", wl.query, wl.q_init)):
+        xv = x[0, :, :n].contiguous()  # bf16 [2, n, 128]
+        c = init.contiguous()          # fp32 [2, K, 128]
+        b, k = c.shape[0], c.shape[1]
+        announce(f"{name} {label}: B={b} N={n} K={k}")
+        xg, cg = xv.to(DEV), c.to(DEV)
+        norms = torch.empty(b, k, device=DEV)
+        labels = torch.empty(b, n, dtype=torch.int32, device=DEV)
+        screened = torch.empty(b, n, k, device=DEV)
+        status = lib.peco_kmeans_screen(_native.ptr(xg), 1, _native.ptr(cg), _native.ptr(norms), _native.ptr(labels),
+                                        _native.ptr(screened), b, n, 128, k, None)
+        assert status == 0
+        torch.cuda.synchronize()
+        x64, c64 = xv.double(), c.double()
+        exact = (c64 * c64).sum(-1)[:, None, :] - 2.0 * torch.bmm(x64, c64.transpose(1, 2))
+        err = (screened.cpu().double() - exact).abs()
+        xn = x64.norm(dim=-1)[:, :, None]
+        cn = c64.norm(dim=-1)[:, None, :]
+        bound = kappa.value * xn * cn + gamma.value * cn * cn
+        ratio = (err / bound).max().item()
+        rel = (err / (xn * cn)).max().item()
+        worst = max(worst, ratio)
+        print(f"[screen] {name} {label}: max |screened - exact| / (|x||c|) = {rel:.3e} "
+              f"(kappa {kappa.value:.3e}); max error / bound = {ratio:.4f}", flush=True)
+        # The labels of this assignment are the canonical ones.
+        ref = canonical.assign(xv.float().numpy(), c.numpy())
+        assert np.array_equal(labels.cpu().numpy(), ref)
+    assert worst < 0.5
