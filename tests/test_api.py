@@ -178,3 +178,23 @@ def test_install_attention_and_reset_state():
     assert ctx.step == -1
     with pytest.raises(ValueError, match="one prompt"):
         pipe.transformer(torch.zeros(1), encoder_attention_mask=torch.ones(2, 4))
+
+
+def test_reference_import_paths_resolve():
+    """The reference's caller imports (generate.py:63-64) and the stage modules resolve
+    through the `peco` package to the very modules of peco_amd."""
+    from peco.model import install_attention, reset_state
+    from peco.processor import PecoConfig
+    from peco.clustering import fit_token_clusters, select_cluster_connections
+    from peco.quantization import fake_quantize_base_offset
+    from peco.attention_cuda import sparse_attention
+    import peco.clustering_cuda
+
+    assert PecoConfig is processor.PecoConfig
+    assert install_attention is model.install_attention and reset_state is model.reset_state
+    assert fit_token_clusters is clustering.fit_token_clusters
+    assert select_cluster_connections is clustering.select_cluster_connections
+    assert fake_quantize_base_offset is quantization.fake_quantize_base_offset
+    assert sparse_attention is attention_cuda.sparse_attention
+    import peco_amd.clustering_cuda
+    assert peco.clustering_cuda is peco_amd.clustering_cuda
