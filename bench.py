@@ -82,8 +82,9 @@ def run_step(layer, wl, q, k, v, q_init, k_init):
 def stage_breakdown(layer, wl, q, k, v, q_init, k_init, reps):
     """Per-stage device time (ms) with events on the current stream, and the realised FLOPs.
 
-    The stages follow ``PecoAttention.attention``: with Base-Offset off the attention reads
-    Q/K/V through the sort permutations and the pack stage is empty.
+    The stages follow ``PecoAttention.attention``: the selection launch also writes the
+    attention's work list (kept-segment lists and ordered items); with Base-Offset off the
+    attention reads Q/K/V through the sort permutations and the pack stage is empty.
     """
     from peco_amd import clustering_cuda, workloads
 
@@ -91,8 +92,8 @@ def stage_breakdown(layer, wl, q, k, v, q_init, k_init, reps):
     n, dim, heads = s.video, s.dims, s.heads
     names = ("kmeans", "select", "pack", "attention")
     acc = {k_: 0.0 for k_ in names}
-    flops = 0.0
     minimum = math.ceil(wl.min_kc_ratio * s.num_k_centroids)
+    length = q.shape[2]
     for _ in range(reps):
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
         ev[0].record()
@@ -100,41 +101,42 @@ def stage_breakdown(layer, wl, q, k, v, q_init, k_init, reps):
         ql, kl, qs, ks = layer._update_cluster_state(q[:, :, :n], k[:, :, :n])
         q_idx, k_idx = layer._last_fit
         ev[1].record()
-        emap, eqs, eks, kept = clustering_cuda.select_connections(
+        work = clustering_cuda.select_work(
             layer.q_centroids.reshape(1, heads, -1, dim), layer.k_centroids.reshape(1, heads, -1, dim), qs, ks,
-            wl.top_p, minimum, text=(s.text, s.text), with_kept=True)
+            wl.top_p, minimum, (s.text, s.text), length, length)
         ev[2].record()
         if s.bits == 0:
-            attn_args = (q, k, v, emap, eqs, eks, q_idx, k_idx, n, kept)
+            attn_args = (q, k, v, work, q_idx, k_idx, n)
         else:
             qp, kp, vp = clustering_cuda.pack_clustered([q, k, v], [q_idx, k_idx, k_idx], [ql, kl, None],
                                                         [layer.q_centroids, layer.k_centroids, None],
                                                         [s.bits, s.bits, 0], n)
-            attn_args = (qp, kp, vp, emap, eqs, eks, q_idx, None, n, kept)
+            attn_args = (qp, kp, vp, work, q_idx, None, n)
         ev[3].record()
         run_attention(attn_args)
         ev[4].record()
         torch.cuda.synchronize()
         for i, nm in enumerate(names):
             acc[nm] += ev[i].elapsed_time(ev[i + 1])
-        flops = workloads.attention_flops(emap, eqs, eks, dim)
+    # Realised F4 from the same selection as a map (outside the timed region).
+    emap, eqs, eks = clustering_cuda.select_connections(
+        layer.q_centroids.reshape(1, heads, -1, dim), layer.k_centroids.reshape(1, heads, -1, dim), qs, ks,
+        wl.top_p, minimum, text=(s.text, s.text))
+    flops = workloads.attention_flops(emap, eqs, eks, dim)
     return {k_: v_ / reps for k_, v_ in acc.items()}, flops, attn_args
 
 
 def run_attention(args_):
-    """The layer's attention launch: indexed inputs when k_index is given, else packed ones."""
+    """The layer's attention launch over the selection's work list: indexed inputs when
+    k_index is given, else packed ones."""
     from peco_amd import attention_cuda
 
-    q, k, v, emap, eqs, eks, q_idx, k_idx, rows, kept = args_
-    if k_idx is None:
-        return attention_cuda.sparse_attention(q, k, v, emap, eqs, eks, validate_sizes=False, out_index=q_idx,
-                                               out_index_rows=rows, kept_keys=kept)
-    return attention_cuda.sparse_attention_indexed(q, k, v, emap, eqs, eks, q_idx, k_idx, rows,
-                                                   validate_sizes=False, kept_keys=kept)
+    q, k, v, work, q_idx, k_idx, rows = args_
+    return attention_cuda.sparse_attention_work(q, k, v, work, out_index=q_idx, out_index_rows=rows, k_index=k_idx)
 
 
 def attention_kernel_time(args_, reps=20):
-    """Average duration of the sparse-attention launch (builder + kernel) on its stream."""
+    """Average duration of the sparse-attention launch on its stream."""
     for _ in range(3):
         run_attention(args_)
     torch.cuda.synchronize()
@@ -400,8 +402,8 @@ def measure(name, steps, warmup, stage_reps, attn_reps=20):
                    "kmeans_iterations": s.iterations, "keep_ratio": s.keep_ratio, "base_offset_bits": s.bits},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic(s.name),
-                     "kernel": ("sparse_attention_indexed" if attn_args[7] is not None else "sparse_attention")
-                     + " (work list + MFMA kernel)", "kernel_ms": round(t_attn, 4),
+                     "kernel": "sparse_attention_kernel, " + ("indexed" if attn_args[5] is not None else "packed")
+                     + " inputs, work list from the selection launch", "kernel_ms": round(t_attn, 4),
                      "flops": flops},
         "stages_ms": {k_: round(v_, 4) for k_, v_ in stages.items()},
         "layer_frac_of_peak": round(value / PEAK_BF16_TFLOPS, 4),

@@ -152,6 +152,38 @@ int peco_select_cluster_connections(const float* qc, const float* kc, const int3
                                     int extend, int valid_text, int text, uint8_t* map, int32_t* ext_q,
                                     int32_t* ext_k, int32_t* kept_keys, void* stream);
 
+/* ABI revision 3 added peco_select_work_size, peco_select_work and
+ * peco_sparse_attention_work. */
+
+/* int32 elements of peco_select_work's work buffer (bh entries, sq query rows, a cq(+2) x
+ * ck(+2) map). */
+size_t peco_select_work_size(int bh, int sq, int cq, int ck, int extend);
+
+/* The selection of peco_select_cluster_connections fused with the attention's work list
+ * (replaces select_cluster_connections, peco/clustering.py:155-186, extend_text_partition,
+ * peco/processor.py:68-84, and the reference's per-launch work map,
+ * peco/kernels/sparse_attention.cu:17-46, whose kernel scans every map row's flags, :94-96).
+ * One launch writes, per map row, the kept-segment list of its key stream (kept clusters with
+ * rows, adjacent ones merged, each as {first physical row - stream offset, stream offset}) and
+ * its stream length, and, per entry, the attention items in cost order (the entry's last
+ * workgroup to finish orders them). map, ext_q and ext_k are optional here. The first bh
+ * int32 of work (8-byte aligned) are arrival counters: zero before the first call on a buffer,
+ * and every call leaves them zero, so one buffer serves calls ordered on a stream but not
+ * overlapping calls. sq and sk are the attention's query and key lengths (video + text). */
+int peco_select_work(const float* qc, const float* kc, const int32_t* q_counts, const int32_t* k_counts, int bh,
+                     int cq, int ck, int dims, float p, int minimum, int extend, int valid_text, int text, int sq,
+                     int sk, uint8_t* map, int32_t* ext_q, int32_t* ext_k, int32_t* work, size_t work_ints,
+                     void* stream);
+
+/* Sparse attention over the work list of peco_select_work (same bh and sq; cq, ck are the
+ * map's dimensions, text groups included): no builder launch and no map read (replaces
+ * peco/kernels/sparse_attention.cu:210 with the work list precomputed). out_index and
+ * k_index as in peco_sparse_attention_ex (k_index null: q/k/v in cluster order) and
+ * peco_sparse_attention_indexed (out_index = q_index: q/k/v in original order). */
+int peco_sparse_attention_work(const void* q, const void* k, const void* v, void* output, const int32_t* out_index,
+                               int out_index_rows, const int32_t* k_index, const int32_t* work, size_t work_ints,
+                               int bh, int sq, int sk, int d, int cq, int ck, int dtype, void* stream);
+
 /* peco_sparse_attention without a workspace argument. No counterpart in the reference: it is
  * for callers that cannot allocate device memory (code under HIP graph capture, serving loops
  * that forbid hipMalloc). The work list lives in a static per-device array of 1048576 int32

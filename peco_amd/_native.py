@@ -126,6 +126,9 @@ SIGNATURES = {
     "peco_sparse_attention_indexed": (I, [P] * 9 + [I, P, P, Z] + [I] * 7 + [P]),
     "peco_select_cluster_connections": (I, [P] * 4 + [I] * 4 + [ctypes.c_float] + [I] * 4 + [P] * 5),
     "peco_sparse_attention_noalloc": (I, [P] * 7 + [I] * 7 + [P]),
+    "peco_select_work_size": (Z, [I] * 5),
+    "peco_select_work": (I, [P] * 4 + [I] * 4 + [ctypes.c_float] + [I] * 6 + [P] * 4 + [Z, P]),
+    "peco_sparse_attention_work": (I, [P] * 5 + [I, P, P, Z] + [I] * 7 + [P]),
 }
 
 

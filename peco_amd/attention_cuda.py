@@ -170,3 +170,60 @@ def sparse_attention_indexed(
     if q_index is None or k_index is None:
         raise ValueError("q_index and k_index are required")
     return _launch(q, k, v, dynamic_map, q_sizes, k_sizes, validate_sizes, q_index, k_index, index_rows, kept_keys)
+
+
+def sparse_attention_work(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    work,
+    *,
+    out_index: torch.Tensor | None = None,
+    out_index_rows: int | None = None,
+    k_index: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """``sparse_attention`` over the work list of ``clustering_cuda.select_work``.
+
+    The key stream of every query cluster comes from its kept-segment list, so no map is
+    read and no builder runs. Without ``k_index`` Q/K/V are in cluster order (as for
+    ``sparse_attention``, with an optional ``out_index`` scatter of the first
+    ``out_index_rows`` output rows); with it, Q/K/V are in original order and read through
+    ``out_index`` (queries, also the output scatter) and ``k_index`` (keys and values), as
+    ``sparse_attention_indexed``.
+    """
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not isinstance(t, torch.Tensor) or not t.is_cuda or not t.is_contiguous() or t.dim() != 4:
+            raise ValueError(f"{name} must be a contiguous 4-D GPU tensor")
+    if q.dtype not in (torch.float16, torch.bfloat16) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("PECO HIP sparse attention supports float16 and bfloat16")
+    batch, heads, sq, dim = q.shape
+    sk = k.shape[2]
+    if k.shape != (batch, heads, sk, dim) or v.shape != k.shape or dim not in (64, 128):
+        raise ValueError("q/k/v shapes must be [B,H,S,D] with D in {64, 128} and matching K/V")
+    if work.bh != batch * heads or work.sq != sq or work.sk != sk:
+        raise ValueError("the work list was built for another shape")
+    output = torch.empty_like(q)
+    if sq == 0:
+        return output
+    rows = sq if out_index_rows is None else int(out_index_rows)
+    if out_index is not None:
+        if not 0 <= rows <= sq:
+            raise ValueError("out_index_rows must be in [0, SQ]")
+        _check_index(out_index, "out_index", batch, heads, rows)
+    if k_index is not None:
+        if out_index is None or rows > sk:
+            raise ValueError("k_index needs out_index and index rows in [0, min(SQ, SK)]")
+        _check_index(k_index, "k_index", batch, heads, rows)
+    with torch.cuda.device(q.device):
+        if not _device_is_gfx950(q.device):
+            raise RuntimeError("This HIP build requires an MI355X-class gfx950 GPU")
+        library = _native.library()
+        stream = _native.current_stream(q.device, q, k, v, work.buffer, output, out_index, k_index)
+        error = library.peco_sparse_attention_work(
+            _native.ptr(q), _native.ptr(k), _native.ptr(v), _native.ptr(output), _native.ptr(out_index), rows,
+            _native.ptr(k_index), _native.ptr(work.buffer), work.ints, batch * heads, sq, sk, dim, work.rows,
+            work.cols, 0 if q.dtype == torch.float16 else 1, stream)
+        if error:
+            message = library.peco_attention_error_string(error).decode("utf-8", errors="replace")
+            raise RuntimeError(f"PECO HIP sparse attention launch failed: {message} ({error})")
+    return output

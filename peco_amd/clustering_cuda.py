@@ -214,6 +214,93 @@ def select_connections(query_centroids, key_centroids, q_counts, k_counts, p, mi
     return dmap, ext_q, ext_k
 
 
+class SelectionWork:
+    """Work list of one peco_select_work launch: the kept-segment list of every map row and
+    the attention items of every (batch, head) in cost order, in ``buffer`` (int32). ``rows``
+    and ``cols`` are the map's dimensions (text groups included), ``sq``/``sk`` the attention's
+    query/key lengths it was built for."""
+
+    def __init__(self, buffer, bh, sq, sk, rows, cols, ints):
+        self.buffer, self.bh, self.sq, self.sk, self.rows, self.cols, self.ints = buffer, bh, sq, sk, rows, cols, ints
+
+    def _layout(self):
+        b, re, ce = self.bh, self.rows, self.cols
+        cap = -(-self.sq // 128) + min(re, self.sq)
+        head = 2 * b + b * re + b * cap * 3
+        head += head & 1
+        return b, re, ce, cap, head
+
+    def tickets(self):
+        return self.buffer[:self.bh]
+
+    def items(self):
+        """(count int32 [bh], items int32 [bh, cap, 3]) as views of the buffer."""
+        b, re, _, cap, _ = self._layout()
+        counts = self.buffer[b:2 * b]
+        items = self.buffer[2 * b + b * re:2 * b + b * re + b * cap * 3].view(b, cap, 3)
+        return counts, items
+
+    def row_lengths(self):
+        b, re, _, _, _ = self._layout()
+        return self.buffer[2 * b:2 * b + b * re].view(b, re)
+
+    def segments(self):
+        """int32 [bh, rows, cols + 2, 2]: per row {count, L}, the segments, the sentinel."""
+        b, re, ce, _, head = self._layout()
+        return self.buffer[head:head + b * re * (ce + 2) * 2].view(b, re, ce + 2, 2)
+
+
+# One work buffer per (device, stream, shape): its arrival counters start at zero and every
+# launch leaves them zero, and launches on one stream are ordered, so they can share it.
+_WORK_BUFFERS = {}
+
+
+def _work_buffer(device, ints, shape):
+    stream = torch.cuda.current_stream(device).cuda_stream
+    key = (device.index, stream, shape)
+    buf = _WORK_BUFFERS.get(key)
+    if buf is None:
+        buf = torch.zeros(ints, dtype=torch.int32, device=device)
+        _WORK_BUFFERS[key] = buf
+    return buf
+
+
+def select_work(query_centroids, key_centroids, q_counts, k_counts, p, minimum, text, sq, sk):
+    """Selection (as ``select_connections``) and the attention's work list in one launch.
+
+    Same inputs as ``select_connections`` with ``text=(valid_text, text_length)`` or None;
+    sq/sk are the attention's query/key lengths (video + text). No map is written: the
+    attention reads each query cluster's kept-segment list instead. Returns a
+    ``SelectionWork`` for ``attention_cuda.sparse_attention_work``.
+    """
+    library = _library()
+    lead = query_centroids.shape[:-2]
+    cq, dims = query_centroids.shape[-2:]
+    ck = key_centroids.shape[-2]
+    bh = 1
+    for n in lead:
+        bh *= n
+    dev = query_centroids.device
+    qc = query_centroids.float().reshape(bh, cq, dims).contiguous()
+    kc = key_centroids.float().reshape(bh, ck, dims).contiguous()
+    qn = q_counts.to(torch.int32).reshape(bh, cq).contiguous()
+    kn = k_counts.to(torch.int32).reshape(bh, ck).contiguous()
+    extend = text is not None
+    valid_text, text_length = text if extend else (0, 0)
+    re, ce = (cq + 2, ck + 2) if extend else (cq, ck)
+    ints = library.peco_select_work_size(bh, int(sq), cq, ck, int(extend))
+    if ints == 0:
+        raise ValueError("invalid selection work shape")
+    with torch.cuda.device(dev):
+        work = _work_buffer(dev, ints, (bh, int(sq), re, ce))
+        status = library.peco_select_work(
+            _native.ptr(qc), _native.ptr(kc), _native.ptr(qn), _native.ptr(kn), bh, cq, ck, dims, float(p),
+            int(minimum), int(extend), int(valid_text), int(text_length), int(sq), int(sk), None, None, None,
+            _native.ptr(work), ints, _retain_on_current_stream(dev, qc, kc, qn, kn, work))
+    _raise_cluster_error(status)
+    return SelectionWork(work, bh, int(sq), int(sk), re, ce, ints)
+
+
 def pack_clustered(tensors, indices, labels, centroids, bits, video):
     """Gather up to three [B,H,S,D] tensors into cluster order in one launch.
 

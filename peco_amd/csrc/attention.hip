@@ -27,6 +27,7 @@
 // An optional out_index writes each output row straight to its original sequence position
 // (fusing restore_sequence_order, peco/clustering.py:128-136).
 #include "common.hpp"
+#include "work.hpp"
 
 #include <algorithm>
 #include <mutex>
@@ -35,10 +36,7 @@
 namespace peco {
 namespace {
 
-// s_waitcnt immediate (gfx9 encoding): vmcnt(1), expcnt unchanged, lgkmcnt(0).
-constexpr int kQTile = 128;   // query rows per item (4 waves x 32)
 constexpr int kKTile = 64;    // keys per LDS tile
-constexpr int kSortCap = 2048;
 constexpr int kSplitRows = 64;  // items up to this many rows pair their waves
 
 struct WorkLayout {
@@ -47,10 +45,6 @@ struct WorkLayout {
     int32_t* items;    // [bh, cap, 3]: q_start, q_cluster, q_rows
     int cap;
 };
-
-__host__ __device__ inline int item_capacity(int sq, int cq) {
-    return static_cast<int>(ceil_div(sq, kQTile)) + min(cq, sq);
-}
 
 __host__ __device__ inline WorkLayout work_layout(int32_t* ws, int bh, int sq, int cq, int ck) {
     WorkLayout w;
@@ -61,40 +55,10 @@ __host__ __device__ inline WorkLayout work_layout(int32_t* ws, int bh, int sq, i
     return w;
 }
 
-__device__ __forceinline__ int wave_incl_scan(int v) {
-    const int lane = lane_id();
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-        const int y = __shfl_up(v, d, kWave);
-        if (lane >= d) v += y;
-    }
-    return v;
-}
-
-// Exclusive scan over a 256-thread block (sum of all values in *total).
-__device__ __forceinline__ int block_scan256(int v, int* tmp, int* total) {
-    const int lane = lane_id();
-    const int wave = threadIdx.x / kWave;
-    const int inc = wave_incl_scan(v);
-    __syncthreads();
-    if (lane == kWave - 1) tmp[wave] = inc;
-    __syncthreads();
-    int base = 0, sum = 0;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        base += w < wave ? tmp[w] : 0;
-        sum += tmp[w];
-    }
-    *total = sum;
-    return base + inc - v;
-}
-
 // Map rows read per wavefront per pass, and bytes of a row per lane per pass (320 keys): one
 // pass covers a head of up to 96 query clusters and 320 key clusters.
 constexpr int kMapRows = 24;
 constexpr int kMapU = 5;
-// Sort payload: query cluster (high bits) and item index within the cluster (low kItemBits).
-constexpr int kItemBits = 12;
 
 // kGivenKept: kept_in [bh, cq] holds each query cluster's kept key rows (from the selection
 // launch), so the map is not read; the counts only order the items.
@@ -174,7 +138,7 @@ __global__ __launch_bounds__(256) void build_work_kernel(const uint8_t* __restri
             }
         }
         int total;
-        int run = block_scan256(local, tmp, &total);
+        int run = block_scan<4>(local, tmp, &total);
         for (int c = c0; c < c1; ++c) {
             const int a = min(sk, run);
             run += ksz[c];
@@ -205,7 +169,7 @@ __global__ __launch_bounds__(256) void build_work_kernel(const uint8_t* __restri
             }
         }
         int total;
-        int run = block_scan256(local, tmp, &total);
+        int run = block_scan<4>(local, tmp, &total);
         for (int c = c0; c < c1; ++c) {
             const int v = qoff[c];
             qoff[c] = min(sq, run);
@@ -242,89 +206,7 @@ __global__ __launch_bounds__(256) void build_work_kernel(const uint8_t* __restri
         }
     }
     __syncthreads();
-    // Items per query cluster.
-    const int per = static_cast<int>(ceil_div(cq, 256));
-    const int c0 = threadIdx.x * per, c1 = min(cq, c0 + per);
-    int local = 0;
-    bool fits = true;  // every item is addressable by the sort payload
-    for (int c = c0; c < c1; ++c) {
-        const int n = static_cast<int>(ceil_div(qoff[c + 1] - qoff[c], kQTile));
-        local += n;
-        fits = fits && n <= (1 << kItemBits);
-    }
-    int count;
-    int slot = block_scan256(local, tmp, &count);
-    const bool sortable = count <= kSortCap && __syncthreads_and(fits) && cq < (1 << (32 - kItemBits));
-    int32_t* items = W.items + static_cast<int64_t>(bh) * W.cap * 3;
-    if (threadIdx.x == 0) W.counts[bh] = count;
-    if (!sortable) {
-        // Cluster order, written directly.
-        for (int c = c0; c < c1; ++c) {
-            const int rows = qoff[c + 1] - qoff[c];
-            for (int r = 0; r < rows; r += kQTile, ++slot) {
-                items[3 * slot + 0] = qoff[c] + r;
-                items[3 * slot + 1] = c;
-                items[3 * slot + 2] = min(kQTile, rows - r);
-            }
-        }
-        return;
-    }
-    for (int c = c0; c < c1; ++c) {
-        const int rows = qoff[c + 1] - qoff[c];
-        for (int r = 0, ri = 0; r < rows; r += kQTile, ++slot, ++ri) {
-            const int n = min(kQTile, rows - r);
-            const uint32_t cost = static_cast<uint32_t>(min<int64_t>(static_cast<int64_t>(n) * kept[c], 0x7fffffff));
-            // (descending cost, cluster, item) for an ascending sort; ties keep cluster order.
-            keys[slot] = (static_cast<uint64_t>(~cost) << 32) | (static_cast<uint32_t>(c) << kItemBits) |
-                         static_cast<uint32_t>(ri);
-        }
-    }
-    __syncthreads();
-    if (count <= 256) {
-        // Rank sort: the keys are distinct, so each one's rank (the number of smaller keys) is
-        // its position. All threads read the same key at a time (LDS broadcast).
-        uint64_t mine = threadIdx.x < count ? keys[threadIdx.x] : ~0ull;
-        int rank = 0;
-        for (int j = 0; j < count; ++j) rank += keys[j] < mine ? 1 : 0;
-        if (threadIdx.x < count) {
-            const uint32_t payload = static_cast<uint32_t>(mine);
-            const int c = static_cast<int>(payload >> kItemBits);
-            const int r = static_cast<int>(payload & ((1u << kItemBits) - 1u)) * kQTile;
-            items[3 * rank + 0] = qoff[c] + r;
-            items[3 * rank + 1] = c;
-            items[3 * rank + 2] = min(kQTile, qoff[c + 1] - qoff[c] - r);
-        }
-        return;
-    }
-    int n2 = 1;
-    while (n2 < count) n2 <<= 1;
-    for (int i = count + threadIdx.x; i < n2; i += 256) keys[i] = ~0ull;
-    __syncthreads();
-    for (int k = 2; k <= n2; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int i = threadIdx.x; i < n2; i += 256) {
-                const int ixj = i ^ j;
-                if (ixj > i) {
-                    const uint64_t a = keys[i], b = keys[ixj];
-                    const bool up = (i & k) == 0;
-                    if ((a > b) == up) {
-                        keys[i] = b;
-                        keys[ixj] = a;
-                    }
-                }
-            }
-            __syncthreads();
-        }
-    }
-    // Items in cost order, rebuilt from the payload.
-    for (int i = threadIdx.x; i < count; i += 256) {
-        const uint32_t payload = static_cast<uint32_t>(keys[i]);
-        const int c = static_cast<int>(payload >> kItemBits);
-        const int r = static_cast<int>(payload & ((1u << kItemBits) - 1u)) * kQTile;
-        items[3 * i + 0] = qoff[c] + r;
-        items[3 * i + 1] = c;
-        items[3 * i + 2] = min(kQTile, qoff[c + 1] - qoff[c] - r);
-    }
+    order_head_items<4>(qoff, kept, cq, W.items + static_cast<int64_t>(bh) * W.cap * 3, W.counts + bh, keys, tmp);
 }
 
 template <int DT> struct Mfma;
@@ -438,10 +320,14 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 // kIndexed: the inputs are in their original token order. Query row j < oi_rows of a head is
 // read from row out_index[j] (the same permutation that scatters the output) and key/value
 // stream row p < oi_rows from row k_index[p]; rows past oi_rows (text) keep their position.
+// The key stream of an item comes either from a kept-segment list (segs, as the selection
+// launch writes it: {count n, stream length L}, n segments, sentinel per map row) or, when segs
+// is null, from the item's map row and the clamped key-cluster prefix kprefix [bh, ck + 1].
 template <int DT, int D, bool kIndexed>
 __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-    const uint8_t* __restrict__ selected, const int32_t* __restrict__ ws, uint16_t* __restrict__ out,
+    const uint8_t* __restrict__ selected, const int32_t* __restrict__ kprefix, const int2* __restrict__ segs,
+    const int32_t* __restrict__ counts, const int32_t* __restrict__ items, int cap, uint16_t* __restrict__ out,
     const int32_t* __restrict__ out_index, int oi_rows, const int32_t* __restrict__ k_index, int bhn, int band,
     int sq, int sk, int cq, int ck, float scale_log2) {
     using T = Tiles<D>;
@@ -464,21 +350,30 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     // a sentinel whose offset no stream row reaches.
     int2* kseg = reinterpret_cast<int2*>(dyn);  // [ck + 1]
 
-    const WorkLayout W = work_layout(const_cast<int32_t*>(ws), bhn, sq, cq, ck);
     // Heads run in bands of `band` (a divisor of bhn), slot-major within a band.
-    const int per_band = band * W.cap;
+    const int per_band = band * cap;
     const int in_band = blockIdx.x % per_band;
     const int bh = (blockIdx.x / per_band) * band + in_band % band;
     const int slot = in_band / band;
-    if (slot >= W.counts[bh]) return;
-    const int32_t* item = W.items + (static_cast<int64_t>(bh) * W.cap + slot) * 3;
+    if (slot >= counts[bh]) return;
+    const int32_t* item = items + (static_cast<int64_t>(bh) * cap + slot) * 3;
     const int q_start = item[0], qc = item[1], q_rows = item[2];
     const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave, h = lane / 32;
 
-    const uint8_t* sel = selected + (static_cast<int64_t>(bh) * cq + qc) * ck;
-    const int32_t* gk = W.kprefix + static_cast<int64_t>(bh) * (ck + 1);
     int L, nk;
-    {
+    if (segs) {
+        // The header and the first 256 entries are loaded together (the row holds ck + 2
+        // entries, so the clamped load stays inside it).
+        const int2* srow = segs + (static_cast<int64_t>(bh) * cq + qc) * (ck + 2);
+        const int2 hdr = srow[0];
+        const int2 first = srow[1 + min(tid, ck)];
+        nk = min(max(hdr.x, 0), ck);
+        L = max(hdr.y, 0);
+        if (tid <= nk) kseg[tid] = first;
+        for (int i = tid + 256; i <= nk; i += 256) kseg[i] = srow[1 + i];
+    } else {
+        const uint8_t* sel = selected + (static_cast<int64_t>(bh) * cq + qc) * ck;
+        const int32_t* gk = kprefix + static_cast<int64_t>(bh) * (ck + 1);
         const int per = static_cast<int>(ceil_div(ck, 256));
         const int c0 = tid * per, c1 = min(ck, c0 + per);
         int local = 0, lcount = 0;
@@ -489,8 +384,8 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
                 ++lcount;
             }
         }
-        int run = block_scan256(local, tmp, &L);
-        int idx = block_scan256(lcount, tmp, &nk);
+        int run = block_scan<4>(local, tmp, &L);
+        int idx = block_scan<4>(lcount, tmp, &nk);
         for (int c = c0; c < c1; ++c) {
             const int a = gk[c], e = gk[c + 1];
             if (sel[c] && e > a) {
@@ -530,7 +425,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     const int prow_entry = 16 * wave + lane % 16;
     const bool prow_owner = lane < 16;
     // Stream position (cluster-order row) of stream row r; rows past the stream read row 0.
-    auto stream_pos = [&](int r) { return r < L ? row_of(r) : 0; };
+    auto stream_pos = [&](int r) { return r < L ? static_cast<int>(min(static_cast<uint32_t>(row_of(r)), sk_last)) : 0; };
     // Physical row of stream position p, given k_index[p] (clamped to the head's rows, so a bad
     // permutation cannot read out of bounds).
     auto physical = [&](int p, int raw) {
@@ -830,6 +725,41 @@ int attention_head_band(int bh, int sk, int d) {
     return 1;
 }
 
+// Launch of the attention kernel over a built work list (map + kprefix, or segs).
+int launch_attention_kernel(const void* q, const void* k, const void* v, const uint8_t* selected,
+                            const int32_t* kprefix, const int2* segs, const int32_t* counts, const int32_t* items,
+                            int cap, void* output, const int32_t* out_index, int out_index_rows,
+                            const int32_t* k_index, int bh, int sq, int sk, int d, int cq, int ck, int dtype,
+                            hipStream_t s) {
+    const size_t lds_attn = sizeof(int) * 2 * (static_cast<size_t>(ck) + 1);
+    const float scale_log2 = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(d)));
+    const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(cap) * bh));
+    const int band = attention_head_band(bh, sk, d);
+    const auto* qp = static_cast<const uint16_t*>(q);
+    const auto* kp = static_cast<const uint16_t*>(k);
+    const auto* vp = static_cast<const uint16_t*>(v);
+    auto* op = static_cast<uint16_t*>(output);
+#define PECO_ATTN(DT_, D_, IX_)                                                                                    \
+    hipLaunchKernelGGL((sparse_attention_kernel<DT_, D_, IX_>), grid, dim3(256), lds_attn, s, qp, kp, vp, selected, \
+                       kprefix, segs, counts, items, cap, op, out_index, out_index_rows, k_index, bh, band, sq, sk,   \
+                       cq, ck, scale_log2)
+#define PECO_ATTN_D(DT_, IX_)                                                                                      \
+    do {                                                                                                           \
+        if (d == 128) PECO_ATTN(DT_, 128, IX_);                                                                    \
+        else PECO_ATTN(DT_, 64, IX_);                                                                              \
+    } while (0)
+    if (dtype == kBF16) {
+        if (k_index) PECO_ATTN_D(kBF16, true);
+        else PECO_ATTN_D(kBF16, false);
+    } else {
+        if (k_index) PECO_ATTN_D(kF16, true);
+        else PECO_ATTN_D(kF16, false);
+    }
+#undef PECO_ATTN_D
+#undef PECO_ATTN
+    return hipGetLastError();
+}
+
 // Shared launcher: k_index (nullable) selects the indexed-input kernel (inputs in original
 // token order, read through out_index for Q and k_index for K/V).
 int launch_sparse_attention(const void* q, const void* k, const void* v, const uint8_t* selected,
@@ -854,32 +784,9 @@ int launch_sparse_attention(const void* q, const void* k, const void* v, const u
     else
         hipLaunchKernelGGL(build_work_kernel<false>, dim3(bh), dim3(256), lds_build, s, selected, q_sizes, k_sizes,
                            nullptr, workspace, bh, sq, sk, cq, ck);
-    const int cap = item_capacity(sq, cq);
-    const float scale_log2 = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(d)));
-    const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(cap) * bh));
-    const int band = attention_head_band(bh, sk, d);
-    const auto* qp = static_cast<const uint16_t*>(q);
-    const auto* kp = static_cast<const uint16_t*>(k);
-    const auto* vp = static_cast<const uint16_t*>(v);
-    auto* op = static_cast<uint16_t*>(output);
-#define PECO_ATTN(DT_, D_, IX_)                                                                                    \
-    hipLaunchKernelGGL((sparse_attention_kernel<DT_, D_, IX_>), grid, dim3(256), lds_attn, s, qp, kp, vp, selected, \
-                       workspace, op, out_index, out_index_rows, k_index, bh, band, sq, sk, cq, ck, scale_log2)
-#define PECO_ATTN_D(DT_, IX_)                                                                                      \
-    do {                                                                                                           \
-        if (d == 128) PECO_ATTN(DT_, 128, IX_);                                                                    \
-        else PECO_ATTN(DT_, 64, IX_);                                                                              \
-    } while (0)
-    if (dtype == kBF16) {
-        if (k_index) PECO_ATTN_D(kBF16, true);
-        else PECO_ATTN_D(kBF16, false);
-    } else {
-        if (k_index) PECO_ATTN_D(kF16, true);
-        else PECO_ATTN_D(kF16, false);
-    }
-#undef PECO_ATTN_D
-#undef PECO_ATTN
-    return hipGetLastError();
+    const WorkLayout W = work_layout(workspace, bh, sq, cq, ck);
+    return launch_attention_kernel(q, k, v, selected, W.kprefix, nullptr, W.counts, W.items, W.cap, output, out_index,
+                                   out_index_rows, k_index, bh, sq, sk, d, cq, ck, dtype, s);
 }
 
 }  // namespace
@@ -911,6 +818,27 @@ PECO_API int peco_sparse_attention_indexed(const void* q, const void* k, const v
     if (index_rows == 0) q_index = k_index = nullptr;  // nothing is permuted
     return launch_sparse_attention(q, k, v, selected, q_sizes, k_sizes, output, q_index, index_rows, k_index, kept_keys,
                                    workspace, workspace_ints, bh, sq, sk, d, cq, ck, dtype, stream);
+}
+
+// Work-list entry: the work list and kept-segment lists come from peco_select_work (same
+// bh, sq and map dims cq x ck), so no builder runs and no map row is read. Q/K/V addressing
+// and out_index/k_index are those of peco_sparse_attention_ex (k_index null) and
+// peco_sparse_attention_indexed (out_index = q_index, k_index given).
+PECO_API int peco_sparse_attention_work(const void* q, const void* k, const void* v, void* output,
+                                        const int32_t* out_index, int out_index_rows, const int32_t* k_index,
+                                        const int32_t* work, size_t work_ints, int bh, int sq, int sk, int d, int cq,
+                                        int ck, int dtype, void* stream) {
+    if (!q || !k || !v || !output || !work || bh < 1 || bh > 65535 || sq < 0 || sk < 0 || cq < 1 || ck < 1 ||
+        (d != 64 && d != 128) || (dtype != kF16 && dtype != kBF16) ||
+        (out_index && (out_index_rows < 0 || out_index_rows > sq)) || (k_index && (!out_index || out_index_rows > sk)))
+        return kInvalidValue;
+    if (sq == 0) return kOk;
+    if (work_ints < sel_work_ints(bh, sq, cq, ck)) return kWorkspaceTooSmall;
+    if (sizeof(int) * 2 * (static_cast<size_t>(ck) + 1) > 24 * 1024) return kUnsupportedShape;
+    const SelWork W = sel_work_layout(const_cast<int32_t*>(work), bh, sq, cq, ck);
+    return launch_attention_kernel(q, k, v, nullptr, nullptr, W.segs, W.counts, W.items, W.cap, output, out_index,
+                                   out_index_rows, k_index, bh, sq, sk, d, cq, ck, dtype,
+                                   static_cast<hipStream_t>(stream));
 }
 
 // Reference ABI (peco/kernels/sparse_attention.cu:210): workspace holds

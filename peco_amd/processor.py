@@ -20,7 +20,7 @@ import torch.nn.functional as F
 from torch.nn.attention import SDPBackend, sdpa_kernel
 
 from . import clustering_cuda
-from .attention_cuda import sparse_attention, sparse_attention_indexed
+from .attention_cuda import sparse_attention, sparse_attention_work
 from .quantization import _validate_bits
 
 
@@ -207,24 +207,24 @@ class PecoAttention:
             query[:, :, :video_length], key[:, :, :video_length])
         q_idx, k_idx = self._last_fit
         # Cluster connectivity from the floating-point centres, extended with the text
-        # partition (select_cluster_connections + extend_text_partition in one launch).
-        dynamic_map, q_sizes, k_sizes, kept = clustering_cuda.select_connections(
+        # partition (select_cluster_connections + extend_text_partition), in one launch that
+        # also writes each query cluster's kept key segments and the attention's work items.
+        work = clustering_cuda.select_work(
             self.q_centroids.reshape(batch, heads, -1, dim), self.k_centroids.reshape(batch, heads, -1, dim),
             q_sizes, k_sizes, self.config.top_p,
-            math.ceil(self.config.min_kc_ratio * self.config.num_k_centroids), text=(valid_text, text_length),
-            with_kept=True)
+            math.ceil(self.config.min_kc_ratio * self.config.num_k_centroids), (valid_text, text_length),
+            length, length)
         if bits == 0:
             # No fake quantization: attention reads Q/K/V through the sort permutations and
             # writes the output in original order, so no packed copy is made.
-            return sparse_attention_indexed(query, key, value, dynamic_map, q_sizes, k_sizes, q_idx, k_idx,
-                                            video_length, validate_sizes=False, kept_keys=kept)
+            return sparse_attention_work(query, key, value, work, out_index=q_idx, out_index_rows=video_length,
+                                         k_index=k_idx)
         # Fake-quantize Q/K against their centroids while packing Q/K/V into cluster order.
         q_perm, k_perm, v_perm = clustering_cuda.pack_clustered(
             [query, key, value], [q_idx, k_idx, k_idx], [q_labels, k_labels, None],
             [self.q_centroids, self.k_centroids, None], [bits, bits, 0], video_length)
         # Video rows return to their original positions; text rows keep theirs.
-        return sparse_attention(q_perm, k_perm, v_perm, dynamic_map, q_sizes, k_sizes, validate_sizes=False,
-                                out_index=q_idx, out_index_rows=video_length, kept_keys=kept)
+        return sparse_attention_work(q_perm, k_perm, v_perm, work, out_index=q_idx, out_index_rows=video_length)
 
     @torch.no_grad()
     def __call__(self, attn, hidden_states, encoder_hidden_states=None, attention_mask=None, image_rotary_emb=None):

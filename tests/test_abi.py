@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_library_loads_and_reports_status_strings_without_a_gpu():
     lib = _native.library()
-    assert lib.peco_abi_version() == 2
+    assert lib.peco_abi_version() == 3
     assert b"workspace" in lib.peco_cluster_error_message(20001)
     assert lib.peco_attention_error_string(0)
     # Size queries are host-only arithmetic.
@@ -50,3 +50,18 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert lib.peco_sparse_attention(null, null, null, null, null, null, null, null, 1, 4, 4, 96, 1, 1, 1,
                                      null) == 1
     assert lib.peco_cluster_sort(null, 1, 4, 2, null, null, null, null, null, 0, null) == 1
+
+
+def test_work_list_entries_reject_bad_arguments_and_size_the_buffer():
+    lib = _native.library()
+    null = ctypes.c_void_p(0)
+    # 24 heads, 7006 rows, a 66 x 258 extended map: counters, counts, row lengths, items
+    # (55 + 66 per head, 3 ints each), then 8-byte aligned segment rows of 260 int2.
+    head = 2 * 24 + 24 * 66 + 24 * (55 + 66) * 3
+    head += head & 1
+    assert lib.peco_select_work_size(24, 7006, 64, 256, 1) == head + 24 * 66 * 260 * 2
+    assert lib.peco_select_work_size(0, 7006, 64, 256, 1) == 0
+    assert lib.peco_select_work(null, null, null, null, 1, 4, 4, 128, 0.5, 0, 0, 0, 0, 16, 16, null, null, null,
+                                null, 1 << 20, null) == 1
+    assert lib.peco_sparse_attention_work(null, null, null, null, null, 0, null, null, 0, 1, 16, 16, 128, 4, 4, 1,
+                                          null) == 1
