@@ -83,14 +83,16 @@ def stage_breakdown(layer, wl, q, k, v, q_init, k_init, reps):
     """Per-stage device time (ms) with events on the current stream, and the realised FLOPs.
 
     The stages follow ``PecoAttention.attention``: the selection launch also writes the
-    attention's work list (kept-segment lists and ordered items); with Base-Offset off the
-    attention reads Q/K/V through the sort permutations and the pack stage is empty.
+    attention's work list (kept-segment lists and ordered items). With Base-Offset off the
+    attention reads Q/K/V through the sort permutations; with it on, the fit's last update
+    also writes K (fake-quantized) and V in key-cluster order, and the attention reads Q
+    through the permutation and fake-quantizes it as it loads it, so there is no pack stage.
     """
     from peco_amd import clustering_cuda, workloads
 
     s = wl.shape
     n, dim, heads = s.video, s.dims, s.heads
-    names = ("kmeans", "select", "pack", "attention")
+    names = ("kmeans", "select", "attention")
     acc = {k_: 0.0 for k_ in names}
     minimum = math.ceil(wl.min_kc_ratio * s.num_k_centroids)
     length = q.shape[2]
@@ -98,7 +100,8 @@ def stage_breakdown(layer, wl, q, k, v, q_init, k_init, reps):
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
         ev[0].record()
         layer.q_centroids, layer.k_centroids = q_init, k_init
-        ql, kl, qs, ks = layer._update_cluster_state(q[:, :, :n], k[:, :, :n])
+        ql, kl, qs, ks = layer._update_cluster_state(q[:, :, :n], k[:, :, :n],
+                                                     pack_keys=(s.bits, k, v) if s.bits else None)
         q_idx, k_idx = layer._last_fit
         ev[1].record()
         work = clustering_cuda.select_work(
@@ -106,15 +109,12 @@ def stage_breakdown(layer, wl, q, k, v, q_init, k_init, reps):
             wl.top_p, minimum, (s.text, s.text), length, length)
         ev[2].record()
         if s.bits == 0:
-            attn_args = (q, k, v, work, q_idx, k_idx, n)
+            attn_args = (q, k, v, work, q_idx, k_idx, n, None, 0)
         else:
-            qp, kp, vp = clustering_cuda.pack_clustered([q, k, v], [q_idx, k_idx, k_idx], [ql, kl, None],
-                                                        [layer.q_centroids, layer.k_centroids, None],
-                                                        [s.bits, s.bits, 0], n)
-            attn_args = (qp, kp, vp, work, q_idx, None, n)
-        ev[3].record()
+            kp, vp = layer._last_pack
+            attn_args = (q, kp, vp, work, q_idx, None, n, layer.q_centroids, s.bits)
         run_attention(attn_args)
-        ev[4].record()
+        ev[3].record()
         torch.cuda.synchronize()
         for i, nm in enumerate(names):
             acc[nm] += ev[i].elapsed_time(ev[i + 1])
@@ -131,8 +131,9 @@ def run_attention(args_):
     k_index is given, else packed ones."""
     from peco_amd import attention_cuda
 
-    q, k, v, work, q_idx, k_idx, rows = args_
-    return attention_cuda.sparse_attention_work(q, k, v, work, out_index=q_idx, out_index_rows=rows, k_index=k_idx)
+    q, k, v, work, q_idx, k_idx, rows, q_centroids, bits = args_
+    return attention_cuda.sparse_attention_work(q, k, v, work, out_index=q_idx, out_index_rows=rows, k_index=k_idx,
+                                                q_centroids=q_centroids, bits=bits)
 
 
 def attention_kernel_time(args_, reps=20):
@@ -402,7 +403,8 @@ def measure(name, steps, warmup, stage_reps, attn_reps=20):
                    "kmeans_iterations": s.iterations, "keep_ratio": s.keep_ratio, "base_offset_bits": s.bits},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic(s.name),
-                     "kernel": "sparse_attention_kernel, " + ("indexed" if attn_args[5] is not None else "packed")
+                     "kernel": "sparse_attention_kernel, " + ("indexed" if attn_args[5] is not None else
+                                                              "K/V packed by the fit, Q quantized at load")
                      + " inputs, work list from the selection launch", "kernel_ms": round(t_attn, 4),
                      "flops": flops},
         "stages_ms": {k_: round(v_, 4) for k_, v_ in stages.items()},

@@ -84,6 +84,20 @@ int peco_kmeans_fit(int num_problems, const void* const* x, const int64_t* x_bat
                     const int* batch, const int* tokens, const int* clusters, int dims, int dtype, int iterations,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* peco_kmeans_fit whose last update also packs (fuses peco/processor.py:141-149 into the
+ * fit): for problem i with hat[i] non-null, hat[i] [batch, length, dims] receives x's rows
+ * in the final cluster order, Base-Offset fake-quantized with bits[i] (4 or 8) against the
+ * final centres, then x's rows [tokens, length) unchanged (the text; x_batch_stride[i] must
+ * cover length rows); with_in[i] -> with_out[i] ([batch, length, dims], both or neither)
+ * are gathered in the same order with their text rows copied. Labels, centres, counts and
+ * the permutation are those of peco_kmeans_fit. (ABI revision 3.) */
+int peco_kmeans_fit_pack(int num_problems, const void* const* x, const int64_t* x_batch_stride,
+                         const float* const* centers_in, float* const* centers_out, int32_t* const* labels,
+                         int32_t* const* counts, int32_t* const* sorted_indices, int32_t* const* offsets,
+                         const int* batch, const int* tokens, const int* clusters, int dims, int dtype, int iterations,
+                         void* const* hat, const int* bits, const void* const* with_in, void* const* with_out,
+                         int length, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Diagnostic of the certified assignment (no counterpart in the reference): for bf16 x
  * [batch, tokens, dims] and fp32 centres, screened[b,t,j] receives the MFMA screen value
  * |c_j|^2 - 2 x_t.c_j (split-bf16 centres) that the assignment compares, labels the certified
@@ -152,8 +166,8 @@ int peco_select_cluster_connections(const float* qc, const float* kc, const int3
                                     int extend, int valid_text, int text, uint8_t* map, int32_t* ext_q,
                                     int32_t* ext_k, int32_t* kept_keys, void* stream);
 
-/* ABI revision 3 added peco_select_work_size, peco_select_work and
- * peco_sparse_attention_work. */
+/* ABI revision 3 added peco_select_work_size, peco_select_work, peco_sparse_attention_work
+ * and peco_kmeans_fit_pack. */
 
 /* int32 elements of peco_select_work's work buffer (bh entries, sq query rows, a cq(+2) x
  * ck(+2) map). */
@@ -179,10 +193,16 @@ int peco_select_work(const float* qc, const float* kc, const int32_t* q_counts, 
  * map's dimensions, text groups included): no builder launch and no map read (replaces
  * peco/kernels/sparse_attention.cu:210 with the work list precomputed). out_index and
  * k_index as in peco_sparse_attention_ex (k_index null: q/k/v in cluster order) and
- * peco_sparse_attention_indexed (out_index = q_index: q/k/v in original order). */
+ * peco_sparse_attention_indexed (out_index = q_index: q/k/v in original order). With
+ * q_centroids (fp32 [bh, q_clusters, d], out_index given, k_index null) k and v are in
+ * cluster order and q in original order: query row j < out_index_rows is read from row
+ * out_index[j] and Base-Offset fake-quantized with `bits` (4 or 8) against the centroid of
+ * its cluster as it is loaded (peco/processor.py:141 and the Q gather fused into the kernel;
+ * the text rows' clusters, q_clusters and up, are not quantized). */
 int peco_sparse_attention_work(const void* q, const void* k, const void* v, void* output, const int32_t* out_index,
-                               int out_index_rows, const int32_t* k_index, const int32_t* work, size_t work_ints,
-                               int bh, int sq, int sk, int d, int cq, int ck, int dtype, void* stream);
+                               int out_index_rows, const int32_t* k_index, const float* q_centroids, int q_clusters,
+                               int bits, const int32_t* work, size_t work_ints, int bh, int sq, int sk, int d, int cq,
+                               int ck, int dtype, void* stream);
 
 /* peco_sparse_attention without a workspace argument. No counterpart in the reference: it is
  * for callers that cannot allocate device memory (code under HIP graph capture, serving loops

@@ -181,6 +181,8 @@ def sparse_attention_work(
     out_index: torch.Tensor | None = None,
     out_index_rows: int | None = None,
     k_index: torch.Tensor | None = None,
+    q_centroids: torch.Tensor | None = None,
+    bits: int = 0,
 ) -> torch.Tensor:
     """``sparse_attention`` over the work list of ``clustering_cuda.select_work``.
 
@@ -189,7 +191,10 @@ def sparse_attention_work(
     ``sparse_attention``, with an optional ``out_index`` scatter of the first
     ``out_index_rows`` output rows); with it, Q/K/V are in original order and read through
     ``out_index`` (queries, also the output scatter) and ``k_index`` (keys and values), as
-    ``sparse_attention_indexed``.
+    ``sparse_attention_indexed``. With ``q_centroids`` (fp32 [B*H, CQ, D]; needs
+    ``out_index``, no ``k_index``) K/V are in cluster order and Q in original order, read
+    through ``out_index`` and Base-Offset fake-quantized with ``bits`` against its cluster's
+    centroid as it is loaded (peco/processor.py:141 and the Q gather fused into the kernel).
     """
     for name, t in (("q", q), ("k", k), ("v", v)):
         if not isinstance(t, torch.Tensor) or not t.is_cuda or not t.is_contiguous() or t.dim() != 4:
@@ -214,15 +219,25 @@ def sparse_attention_work(
         if out_index is None or rows > sk:
             raise ValueError("k_index needs out_index and index rows in [0, min(SQ, SK)]")
         _check_index(k_index, "k_index", batch, heads, rows)
+    q_clusters = 0
+    if q_centroids is not None:
+        if out_index is None or k_index is not None or bits not in (4, 8):
+            raise ValueError("q_centroids needs out_index, no k_index and bits in {4, 8}")
+        if q_centroids.dtype != torch.float32 or not q_centroids.is_contiguous() or q_centroids.dim() != 3 \
+                or q_centroids.shape[0] != batch * heads or q_centroids.shape[2] != dim \
+                or not 1 <= q_centroids.shape[1] <= work.rows or q_centroids.device != q.device:
+            raise ValueError("q_centroids must be contiguous fp32 [B*H, CQ, D] on the device of q")
+        q_clusters = q_centroids.shape[1]
     with torch.cuda.device(q.device):
         if not _device_is_gfx950(q.device):
             raise RuntimeError("This HIP build requires an MI355X-class gfx950 GPU")
         library = _native.library()
-        stream = _native.current_stream(q.device, q, k, v, work.buffer, output, out_index, k_index)
+        stream = _native.current_stream(q.device, q, k, v, work.buffer, output, out_index, k_index, q_centroids)
         error = library.peco_sparse_attention_work(
             _native.ptr(q), _native.ptr(k), _native.ptr(v), _native.ptr(output), _native.ptr(out_index), rows,
-            _native.ptr(k_index), _native.ptr(work.buffer), work.ints, batch * heads, sq, sk, dim, work.rows,
-            work.cols, 0 if q.dtype == torch.float16 else 1, stream)
+            _native.ptr(k_index), _native.ptr(q_centroids), q_clusters, int(bits) if q_centroids is not None else 0,
+            _native.ptr(work.buffer), work.ints, batch * heads, sq, sk, dim, work.rows, work.cols,
+            0 if q.dtype == torch.float16 else 1, stream)
         if error:
             message = library.peco_attention_error_string(error).decode("utf-8", errors="replace")
             raise RuntimeError(f"PECO HIP sparse attention launch failed: {message} ({error})")

@@ -129,11 +129,19 @@ class KMeansProblem:
         self.clusters = self.init.shape[1]
 
 
-def kmeans_fit(problems, iterations):
+def kmeans_fit(problems, iterations, pack=None):
     """Fused Lloyd fit of one or two problems in shared launches.
 
     Returns, per problem, (labels int32 [B,N], centers fp32 [B,K,D], counts int32 [B,K],
     indices int32 [B,N], offsets int32 [B,K+1]); indices is the stable sort of labels.
+
+    ``pack`` (optional, one entry per problem, None or ``(bits, length, with_tensor)``) makes
+    the last update also pack that problem (peco/processor.py:141-149 fused into the fit):
+    hat [B, length, D] receives x's rows in the final cluster order, Base-Offset
+    fake-quantized with ``bits`` against the final centres, then x's rows [N, length) (the
+    text, which x's batch stride must cover); ``with_tensor`` ([B, length, D] or None) is
+    gathered in the same order into a new tensor. Then returns (outs, packed) with packed[i] =
+    (hat, with_out) or None.
     """
     library = _library()
     if not 1 <= len(problems) <= 2:
@@ -143,6 +151,8 @@ def kmeans_fit(problems, iterations):
     dev = problems[0].x.device
     if any(p.dims != dims or p.x.dtype != dtype or p.x.device != dev for p in problems):
         raise ValueError("kmeans_fit problems must share dims, dtype and device")
+    if pack is not None and len(pack) != len(problems):
+        raise ValueError("pack needs one entry per problem")
     outs = []
     ws_bytes = 0
     for p in problems:
@@ -157,20 +167,51 @@ def kmeans_fit(problems, iterations):
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     strides = (ctypes.c_int64 * len(problems))(*[p.x.stride(0) for p in problems])
     tensors = [p.x for p in problems] + [p.init for p in problems] + [t for o in outs for t in o] + [ws]
+    common = (
+        len(problems),
+        _native.ptr_array([p.x for p in problems]), ctypes.cast(strides, ctypes.c_void_p),
+        _native.ptr_array([p.init for p in problems]),
+        _native.ptr_array([o[1] for o in outs]), _native.ptr_array([o[0] for o in outs]),
+        _native.ptr_array([o[2] for o in outs]), _native.ptr_array([o[3] for o in outs]),
+        _native.ptr_array([o[4] for o in outs]),
+        _native.int_array([p.batch for p in problems]), _native.int_array([p.tokens for p in problems]),
+        _native.int_array([p.clusters for p in problems]), dims, _DTYPES[dtype], int(iterations),
+    )
+    if pack is None:
+        with torch.cuda.device(dev):
+            status = library.peco_kmeans_fit(*common, _native.ptr(ws), ws_bytes,
+                                             _retain_on_current_stream(dev, *tensors))
+        _raise_cluster_error(status)
+        return outs
+    length = None
+    hats, withs_in, withs_out, bits = [], [], [], []
+    for p, spec in zip(problems, pack):
+        if spec is None:
+            hats.append(None), withs_in.append(None), withs_out.append(None), bits.append(0)
+            continue
+        b, n, w = spec
+        if length is not None and n != length:
+            raise ValueError("packed problems must share one length")
+        length = int(n)
+        if length < p.tokens or (length > p.tokens and p.x.stride(0) < length * dims):
+            raise ValueError("x's batch stride must cover the packed length")
+        hats.append(torch.empty((p.batch, length, dims), dtype=dtype, device=dev))
+        if w is not None:
+            if w.shape != (p.batch, length, dims) or w.dtype != dtype or not w.is_contiguous() or w.device != dev:
+                raise ValueError("the gathered companion must be a contiguous [B, length, D] tensor like x")
+            withs_out.append(torch.empty_like(w))
+        else:
+            withs_out.append(None)
+        withs_in.append(w)
+        bits.append(int(b))
     with torch.cuda.device(dev):
-        status = library.peco_kmeans_fit(
-            len(problems),
-            _native.ptr_array([p.x for p in problems]), ctypes.cast(strides, ctypes.c_void_p),
-            _native.ptr_array([p.init for p in problems]),
-            _native.ptr_array([o[1] for o in outs]), _native.ptr_array([o[0] for o in outs]),
-            _native.ptr_array([o[2] for o in outs]), _native.ptr_array([o[3] for o in outs]),
-            _native.ptr_array([o[4] for o in outs]),
-            _native.int_array([p.batch for p in problems]), _native.int_array([p.tokens for p in problems]),
-            _native.int_array([p.clusters for p in problems]), dims, _DTYPES[dtype], int(iterations),
-            _native.ptr(ws), ws_bytes, _retain_on_current_stream(dev, *tensors),
-        )
+        status = library.peco_kmeans_fit_pack(
+            *common, _native.ptr_array(hats), _native.int_array(bits), _native.ptr_array(withs_in),
+            _native.ptr_array(withs_out), int(length or 0), _native.ptr(ws), ws_bytes,
+            _retain_on_current_stream(dev, *tensors, *[t for t in hats + withs_in + withs_out if t is not None]))
     _raise_cluster_error(status)
-    return outs
+    packed = [None if h is None else (h, w) for h, w in zip(hats, withs_out)]
+    return outs, packed
 
 
 def select_connections(query_centroids, key_centroids, q_counts, k_counts, p, minimum, text=None, *,

@@ -26,6 +26,7 @@
 // P is rounded to the input dtype before the PV product (the reference keeps P in fp32).
 // An optional out_index writes each output row straight to its original sequence position
 // (fusing restore_sequence_order, peco/clustering.py:128-136).
+#include "base_offset.hpp"
 #include "common.hpp"
 #include "work.hpp"
 
@@ -317,19 +318,30 @@ __device__ __forceinline__ void load_tile_lds(uint16_t* ks, uint16_t* vs, const 
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
-// kIndexed: the inputs are in their original token order. Query row j < oi_rows of a head is
-// read from row out_index[j] (the same permutation that scatters the output) and key/value
-// stream row p < oi_rows from row k_index[p]; rows past oi_rows (text) keep their position.
+// Input modes:
+//   kPacked: Q, K and V in cluster order (out_index, when given, only scatters the output);
+//   kIndexed: the inputs are in their original token order. Query row j < oi_rows of a head
+//     is read from row out_index[j] (the same permutation that scatters the output) and
+//     key/value stream row p < oi_rows from row k_index[p]; rows past oi_rows (text) keep
+//     their position;
+//   kQuantQ: K and V in cluster order, Q in original order read through out_index as in
+//     kIndexed and Base-Offset fake-quantized as it is loaded: every row of an item belongs
+//     to its query cluster qc, so rows of a video cluster (qc < qcent_rows) take centroid
+//     qcent[bh, qc] and levels = 2^bits - 1 (peco/processor.py:141, fused into the load).
 // The key stream of an item comes either from a kept-segment list (segs, as the selection
 // launch writes it: {count n, stream length L}, n segments, sentinel per map row) or, when segs
 // is null, from the item's map row and the clamped key-cluster prefix kprefix [bh, ck + 1].
-template <int DT, int D, bool kIndexed>
+enum InputMode : int { kPacked = 0, kIndexed = 1, kQuantQ = 2 };
+
+template <int DT, int D, int kMode>
 __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint8_t* __restrict__ selected, const int32_t* __restrict__ kprefix, const int2* __restrict__ segs,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ items, int cap, uint16_t* __restrict__ out,
-    const int32_t* __restrict__ out_index, int oi_rows, const int32_t* __restrict__ k_index, int bhn, int band,
-    int sq, int sk, int cq, int ck, float scale_log2) {
+    const int32_t* __restrict__ out_index, int oi_rows, const int32_t* __restrict__ k_index,
+    const float* __restrict__ qcent, int qcent_rows, float levels, int bhn, int band, int sq, int sk, int cq,
+    int ck, float scale_log2) {
+    constexpr bool kIndexedKV = kMode == kIndexed;
     using T = Tiles<D>;
     constexpr int S = D / 16;       // k-steps of S^T over channels
     constexpr int NB = D / 32;      // 32-channel blocks of O^T
@@ -359,14 +371,60 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     const int32_t* item = items + (static_cast<int64_t>(bh) * cap + slot) * 3;
     const int q_start = item[0], qc = item[1], q_rows = item[2];
     const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave, h = lane / 32;
+    const int64_t head = static_cast<int64_t>(bh);
+    const uint32_t sq_last = static_cast<uint32_t>(sq - 1), sk_last = static_cast<uint32_t>(sk - 1);
 
+    // Items of at most kSplitRows rows pair the waves: wave w takes 32-row block w & 1 and, of
+    // every tile, only the 32-key half w >> 1, so a short item's tiles cost about half the
+    // time; each pair merges its two partial softmax states after the last tile. Longer items
+    // give each wave its own row block and both halves of every tile.
+    const bool split = q_rows <= kSplitRows;
+    const int rb = split ? (wave & 1) : wave;  // this wave's 32-row block
+    const int hb = split ? (wave >> 1) : 0;    // first 32-key half this wave processes
+    // Waves without query rows issue every tile load, so that waiting for the load path to
+    // accept them never delays a wave with MFMA work; with no such wave all four share.
+    const int row_blocks = static_cast<int>(ceil_div(q_rows, 32));
+    const int idle = split ? 4 - 2 * row_blocks : 4 - row_blocks;   // waves 4-idle .. 3 (or 1, 3)
+    const int loaders = idle >= 2 ? 2 : (idle == 1 ? 1 : 4);
+    int loader_rank;
+    if (loaders == 4) loader_rank = wave;
+    else if (split) loader_rank = (wave & 1) ? wave >> 1 : -1;   // idle waves 1 and 3
+    else loader_rank = wave >= 4 - loaders ? wave - (4 - loaders) : -1;
+    // Q^T operand: lane holds query row (32*rb + l%32), channels 16s + 8h .. +7. Its loads
+    // (and the permutation entry they depend on) go out before the key stream's, so their
+    // latency overlaps the stream setup below.
+    const int qrow = rb * 32 + (lane % 32);
+    const bool qvalid = qrow < q_rows;
+    const bool wave_active = rb * 32 < q_rows;
+    int64_t qsrc = q_start + qrow;
+    if constexpr (kMode != kPacked) {
+        if (qvalid && qsrc < oi_rows) qsrc = min(static_cast<uint32_t>(out_index[head * oi_rows + qsrc]), sq_last);
+    }
+    // The segment list's header and first 256 entries (the row holds ck + 2 entries, so the
+    // clamped load stays inside it) are requested before the query rows, which wait for the
+    // permutation entry.
+    const int2* srow = segs ? segs + (static_cast<int64_t>(bh) * cq + qc) * (ck + 2) : nullptr;
+    int2 hdr{0, 0}, first{0, 0};
+    if (segs) {
+        hdr = srow[0];
+        first = srow[1 + min(tid, ck)];
+    }
+    u16x8 qf[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        qf[s] = qvalid ? *reinterpret_cast<const u16x8*>(q + (head * sq + qsrc) * D + 16 * s + 8 * h)
+                       : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+    // kQuantQ: the centroid channels of this lane's half row (every row of the item has the
+    // item's query cluster), requested with the rows.
+    f32x8 qc_row[kMode == kQuantQ ? S : 1];
+    if constexpr (kMode == kQuantQ) {
+        const float* crow = qcent + (head * qcent_rows + min(qc, qcent_rows - 1)) * D + 8 * h;
+#pragma unroll
+        for (int s = 0; s < S; ++s) qc_row[s] = *reinterpret_cast<const f32x8*>(crow + 16 * s);
+    }
     int L, nk;
     if (segs) {
-        // The header and the first 256 entries are loaded together (the row holds ck + 2
-        // entries, so the clamped load stays inside it).
-        const int2* srow = segs + (static_cast<int64_t>(bh) * cq + qc) * (ck + 2);
-        const int2 hdr = srow[0];
-        const int2 first = srow[1 + min(tid, ck)];
         nk = min(max(hdr.x, 0), ck);
         L = max(hdr.y, 0);
         if (tid <= nk) kseg[tid] = first;
@@ -419,9 +477,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     // into pidx at the end of tile t and used at the end of tile t+1. Every load of the loop
     // goes straight to LDS (no register is written behind the compiler's back), so the loop
     // waits for them explicitly.
-    const int64_t head = static_cast<int64_t>(bh);
-    const int32_t* kidx = kIndexed ? k_index + head * oi_rows : nullptr;
-    const uint32_t sq_last = static_cast<uint32_t>(sq - 1), sk_last = static_cast<uint32_t>(sk - 1);
+    const int32_t* kidx = kIndexedKV ? k_index + head * oi_rows : nullptr;
     const int prow_entry = 16 * wave + lane % 16;
     const bool prow_owner = lane < 16;
     // Stream position (cluster-order row) of stream row r; rows past the stream read row 0.
@@ -429,12 +485,12 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     // Physical row of stream position p, given k_index[p] (clamped to the head's rows, so a bad
     // permutation cannot read out of bounds).
     auto physical = [&](int p, int raw) {
-        if constexpr (kIndexed) return p < oi_rows ? static_cast<int>(min(static_cast<uint32_t>(raw), sk_last)) : p;
+        if constexpr (kIndexedKV) return p < oi_rows ? static_cast<int>(min(static_cast<uint32_t>(raw), sk_last)) : p;
         else return p;
     };
     auto stream_row = [&](int r) {
         const int p = stream_pos(r);
-        if constexpr (kIndexed) return physical(p, kidx[min(p, oi_rows - 1)]);
+        if constexpr (kIndexedKV) return physical(p, kidx[min(p, oi_rows - 1)]);
         else return p;
     };
     int p2 = 0;  // indexed: this lane's stream position in tile t+2 (its k_index value is in pidx)
@@ -442,41 +498,11 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
         prow[0][prow_entry] = stream_row(prow_entry);
         prow[1][prow_entry] = stream_row(kKTile + prow_entry);
     }
-    if constexpr (kIndexed) {
+    if constexpr (kIndexedKV) {
         p2 = stream_pos(2 * kKTile + prow_entry);
         if (prow_owner) pidx[1][prow_entry] = kidx[min(p2, oi_rows - 1)];
     }
 
-    // Items of at most kSplitRows rows pair the waves: wave w takes 32-row block w & 1 and, of
-    // every tile, only the 32-key half w >> 1, so a short item's tiles cost about half the
-    // time; each pair merges its two partial softmax states after the last tile. Longer items
-    // give each wave its own row block and both halves of every tile.
-    const bool split = q_rows <= kSplitRows;
-    const int rb = split ? (wave & 1) : wave;  // this wave's 32-row block
-    const int hb = split ? (wave >> 1) : 0;    // first 32-key half this wave processes
-    // Waves without query rows issue every tile load, so that waiting for the load path to
-    // accept them never delays a wave with MFMA work; with no such wave all four share.
-    const int row_blocks = static_cast<int>(ceil_div(q_rows, 32));
-    const int idle = split ? 4 - 2 * row_blocks : 4 - row_blocks;   // waves 4-idle .. 3 (or 1, 3)
-    const int loaders = idle >= 2 ? 2 : (idle == 1 ? 1 : 4);
-    int loader_rank;
-    if (loaders == 4) loader_rank = wave;
-    else if (split) loader_rank = (wave & 1) ? wave >> 1 : -1;   // idle waves 1 and 3
-    else loader_rank = wave >= 4 - loaders ? wave - (4 - loaders) : -1;
-    // Q^T operand: lane holds query row (32*rb + l%32), channels 16s + 8h .. +7.
-    const int qrow = rb * 32 + (lane % 32);
-    const bool qvalid = qrow < q_rows;
-    const bool wave_active = rb * 32 < q_rows;
-    int64_t qsrc = q_start + qrow;
-    if constexpr (kIndexed) {
-        if (qvalid && qsrc < oi_rows) qsrc = min(static_cast<uint32_t>(out_index[head * oi_rows + qsrc]), sq_last);
-    }
-    u16x8 qf[S];
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-        qf[s] = qvalid ? *reinterpret_cast<const u16x8*>(q + (head * sq + qsrc) * D + 16 * s + 8 * h)
-                       : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
-    }
     f32x16 oacc[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) oacc[nb] = f32x16{};
@@ -595,8 +621,46 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
             }
         }
     };
+    if constexpr (kMode == kQuantQ) {
+        // The query rows and centroid must arrive before the tile loads below are issued: the
+        // compiler does not count those loads, so a later wait for the rows would also wait
+        // for the tile.
+#if defined(__HIP_DEVICE_COMPILE__)
+#pragma unroll
+        for (int s = 0; s < S; ++s) asm volatile("" ::"v"(qf[s]), "v"(qc_row[s]));
+#endif
+    }
     __syncthreads();
     if (ntiles > 0) load_tile_lds<D, 4>(ks[0], vs[0], kh, vh, prow[0], wave, lane);
+    if constexpr (kMode == kQuantQ) {
+        if (qc < qcent_rows) {
+            // This lane holds channels 16s + 8h .. +7 of its row and lane l ^ 32 the others:
+            // the row's residual bounds are the two lanes' bounds combined. All of it is VALU
+            // work on registers that arrived before the first tile's loads were issued, so it
+            // runs while those loads are in flight.
+            float lo = INFINITY, hi = -INFINITY;
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float r = half_to_f32<DT>(qf[s][i]) - qc_row[s][i];
+                    lo = fminf(lo, r);
+                    hi = fmaxf(hi, r);
+                }
+            lo = fminf(lo, __shfl_xor(lo, 32, kWave));
+            hi = fmaxf(hi, __shfl_xor(hi, 32, kWave));
+            const BaseOffsetRow bo = base_offset_row(lo, hi, levels);
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float c = qc_row[s][i];
+                    uint32_t code;
+                    const float xh = base_offset_value(half_to_f32<DT>(qf[s][i]) - c, c, bo, code);
+                    qf[s][i] = f32_to_half<DT>(xh);
+                }
+        }
+    }
     __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0): this wave's tile-0 loads have landed
     __syncthreads();
     auto step = [&](auto bufc, int tile) __attribute__((always_inline)) {
@@ -617,7 +681,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
             else if (loaders == 2) load_tile_lds<D, 2>(ks[buf ^ 1], vs[buf ^ 1], kh, vh, prow[buf ^ 1], loader_rank, lane);
             else load_tile_lds<D, 1>(ks[buf ^ 1], vs[buf ^ 1], kh, vh, prow[buf ^ 1], loader_rank, lane);
         }
-        if constexpr (kIndexed) {
+        if constexpr (kIndexedKV) {
             const int p3 = stream_pos((tile + 3) * kKTile + prow_entry);
             if (prow_owner) dma4(kidx + min(p3, oi_rows - 1), lds_addr(&pidx[buf][16 * wave]));
             // Everything but that index load has landed: this wave's tile t+1 loads and the
@@ -726,11 +790,14 @@ int attention_head_band(int bh, int sk, int d) {
 }
 
 // Launch of the attention kernel over a built work list (map + kprefix, or segs).
+// q_centroids (nullable, with out_index and no k_index) selects the kQuantQ input mode.
 int launch_attention_kernel(const void* q, const void* k, const void* v, const uint8_t* selected,
                             const int32_t* kprefix, const int2* segs, const int32_t* counts, const int32_t* items,
                             int cap, void* output, const int32_t* out_index, int out_index_rows,
-                            const int32_t* k_index, int bh, int sq, int sk, int d, int cq, int ck, int dtype,
-                            hipStream_t s) {
+                            const int32_t* k_index, const float* q_centroids, int q_clusters, int bits, int bh,
+                            int sq, int sk, int d, int cq, int ck, int dtype, hipStream_t s) {
+    const int mode = k_index ? kIndexed : (q_centroids ? kQuantQ : kPacked);
+    const float levels = static_cast<float>((1 << bits) - 1);
     const size_t lds_attn = sizeof(int) * 2 * (static_cast<size_t>(ck) + 1);
     const float scale_log2 = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(d)));
     const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(cap) * bh));
@@ -739,22 +806,24 @@ int launch_attention_kernel(const void* q, const void* k, const void* v, const u
     const auto* kp = static_cast<const uint16_t*>(k);
     const auto* vp = static_cast<const uint16_t*>(v);
     auto* op = static_cast<uint16_t*>(output);
-#define PECO_ATTN(DT_, D_, IX_)                                                                                    \
-    hipLaunchKernelGGL((sparse_attention_kernel<DT_, D_, IX_>), grid, dim3(256), lds_attn, s, qp, kp, vp, selected, \
-                       kprefix, segs, counts, items, cap, op, out_index, out_index_rows, k_index, bh, band, sq, sk,   \
-                       cq, ck, scale_log2)
-#define PECO_ATTN_D(DT_, IX_)                                                                                      \
+#define PECO_ATTN(DT_, D_, M_)                                                                                     \
+    hipLaunchKernelGGL((sparse_attention_kernel<DT_, D_, M_>), grid, dim3(256), lds_attn, s, qp, kp, vp, selected,  \
+                       kprefix, segs, counts, items, cap, op, out_index, out_index_rows, k_index, q_centroids,       \
+                       q_clusters, levels, bh, band, sq, sk, cq, ck, scale_log2)
+#define PECO_ATTN_D(DT_, M_)                                                                                       \
     do {                                                                                                           \
-        if (d == 128) PECO_ATTN(DT_, 128, IX_);                                                                    \
-        else PECO_ATTN(DT_, 64, IX_);                                                                              \
+        if (d == 128) PECO_ATTN(DT_, 128, M_);                                                                     \
+        else PECO_ATTN(DT_, 64, M_);                                                                               \
     } while (0)
-    if (dtype == kBF16) {
-        if (k_index) PECO_ATTN_D(kBF16, true);
-        else PECO_ATTN_D(kBF16, false);
-    } else {
-        if (k_index) PECO_ATTN_D(kF16, true);
-        else PECO_ATTN_D(kF16, false);
-    }
+#define PECO_ATTN_M(DT_)                                                                                           \
+    do {                                                                                                           \
+        if (mode == kIndexed) PECO_ATTN_D(DT_, kIndexed);                                                          \
+        else if (mode == kQuantQ) PECO_ATTN_D(DT_, kQuantQ);                                                       \
+        else PECO_ATTN_D(DT_, kPacked);                                                                            \
+    } while (0)
+    if (dtype == kBF16) PECO_ATTN_M(kBF16);
+    else PECO_ATTN_M(kF16);
+#undef PECO_ATTN_M
 #undef PECO_ATTN_D
 #undef PECO_ATTN
     return hipGetLastError();
@@ -786,7 +855,7 @@ int launch_sparse_attention(const void* q, const void* k, const void* v, const u
                            nullptr, workspace, bh, sq, sk, cq, ck);
     const WorkLayout W = work_layout(workspace, bh, sq, cq, ck);
     return launch_attention_kernel(q, k, v, selected, W.kprefix, nullptr, W.counts, W.items, W.cap, output, out_index,
-                                   out_index_rows, k_index, bh, sq, sk, d, cq, ck, dtype, s);
+                                   out_index_rows, k_index, nullptr, 0, 0, bh, sq, sk, d, cq, ck, dtype, s);
 }
 
 }  // namespace
@@ -823,21 +892,27 @@ PECO_API int peco_sparse_attention_indexed(const void* q, const void* k, const v
 // Work-list entry: the work list and kept-segment lists come from peco_select_work (same
 // bh, sq and map dims cq x ck), so no builder runs and no map row is read. Q/K/V addressing
 // and out_index/k_index are those of peco_sparse_attention_ex (k_index null) and
-// peco_sparse_attention_indexed (out_index = q_index, k_index given).
+// peco_sparse_attention_indexed (out_index = q_index, k_index given). With q_centroids
+// (fp32 [bh, q_clusters, d]; needs out_index and no k_index) K and V are in cluster order and
+// Q in original order: query row j < out_index_rows is read from row out_index[j] and
+// Base-Offset fake-quantized with `bits` against its cluster's centroid as it is loaded.
 PECO_API int peco_sparse_attention_work(const void* q, const void* k, const void* v, void* output,
                                         const int32_t* out_index, int out_index_rows, const int32_t* k_index,
-                                        const int32_t* work, size_t work_ints, int bh, int sq, int sk, int d, int cq,
-                                        int ck, int dtype, void* stream) {
+                                        const float* q_centroids, int q_clusters, int bits, const int32_t* work,
+                                        size_t work_ints, int bh, int sq, int sk, int d, int cq, int ck, int dtype,
+                                        void* stream) {
     if (!q || !k || !v || !output || !work || bh < 1 || bh > 65535 || sq < 0 || sk < 0 || cq < 1 || ck < 1 ||
         (d != 64 && d != 128) || (dtype != kF16 && dtype != kBF16) ||
-        (out_index && (out_index_rows < 0 || out_index_rows > sq)) || (k_index && (!out_index || out_index_rows > sk)))
+        (out_index && (out_index_rows < 0 || out_index_rows > sq)) || (k_index && (!out_index || out_index_rows > sk)) ||
+        (q_centroids && (!out_index || k_index || q_clusters < 1 || q_clusters > cq || (bits != 4 && bits != 8))))
         return kInvalidValue;
     if (sq == 0) return kOk;
     if (work_ints < sel_work_ints(bh, sq, cq, ck)) return kWorkspaceTooSmall;
     if (sizeof(int) * 2 * (static_cast<size_t>(ck) + 1) > 24 * 1024) return kUnsupportedShape;
     const SelWork W = sel_work_layout(const_cast<int32_t*>(work), bh, sq, cq, ck);
     return launch_attention_kernel(q, k, v, nullptr, nullptr, W.segs, W.counts, W.items, W.cap, output, out_index,
-                                   out_index_rows, k_index, bh, sq, sk, d, cq, ck, dtype,
+                                   out_index_rows, k_index, q_centroids, q_centroids ? q_clusters : 0,
+                                   q_centroids ? bits : 0, bh, sq, sk, d, cq, ck, dtype,
                                    static_cast<hipStream_t>(stream));
 }
 

@@ -25,6 +25,7 @@
 // sort place (stable counting sort, also yields the final permutation for stage 3) ->
 // update (sequential per-cluster sums in token order; also prepares the next iteration's
 // split-bf16 centres and canonical norms). Q and K fits share every launch.
+#include "base_offset.hpp"
 #include "common.hpp"
 #include "sort.hpp"
 
@@ -60,6 +61,16 @@ struct KmProblem {
     int upd_begin;          // first linear km_update_kernel workgroup of this problem
     int upd_blocks;
     int upd_shared;         // 1: one workgroup per cluster, 0: one wavefront per cluster
+    // Packing by the last update (nullable hat): rows [0, tokens) of hat [batch, length, D]
+    // receive x's rows in cluster order, Base-Offset fake-quantized (hat_bits) against the
+    // final centres, and rows [tokens, length) x's own rows past `tokens` (text, in the same
+    // batch stride); with_in/with_out (nullable, [batch, length, D]) are gathered alike
+    // without quantization.
+    void* hat;
+    const void* with_in;
+    void* with_out;
+    int hat_bits;
+    int length;
 };
 
 constexpr int kMaxKm = 2;
@@ -74,6 +85,7 @@ struct KmArgs {
     int total_update_blocks;
     int total_scan_blocks;
     int total_upd_blocks;
+    int text_blocks;  // packing launch only: workgroups after the update's that copy text rows
     float kappa;      // bound coefficient: |screened - canonical| <= kappa*|x||c| + rounding terms
     float gamma_acc;  // gamma of the MFMA accumulation length (applied to the norm term)
 };
@@ -773,11 +785,101 @@ __device__ __forceinline__ int km_update_problem(const KmArgs& a, int block) {
     return p;
 }
 
+// Packing pass of the last update: the members of one cluster, in sorted order m (= their
+// packed row), 16 lanes per row (8 channels each; 8 lanes at D = 64). The members go 64 at
+// a time (`first`, `stride`: this wavefront's first member and step); one index load per
+// lane, then the rows of 8 passes (32 or 64 rows) are requested together before any is used.
+template <int DT> struct Raw8 {
+    u32x4 v[DT == kF32 ? 2 : 1];
+    __device__ __forceinline__ void load(const void* base, int64_t e) {
+        const u32x4* p = reinterpret_cast<const u32x4*>(static_cast<const char*>(base) + e * (DT == kF32 ? 4 : 2));
+#pragma unroll
+        for (int i = 0; i < (DT == kF32 ? 2 : 1); ++i) v[i] = p[i];
+    }
+    __device__ __forceinline__ void store(void* base, int64_t e) const {
+        u32x4* p = reinterpret_cast<u32x4*>(static_cast<char*>(base) + e * (DT == kF32 ? 4 : 2));
+#pragma unroll
+        for (int i = 0; i < (DT == kF32 ? 2 : 1); ++i) p[i] = v[i];
+    }
+};
+
 template <int DT, int D>
+__device__ __forceinline__ void pack_members(const KmProblem& P, int b, int begin, int end, const float* centre,
+                                             int first, int stride) {
+    constexpr int G = D / 8;       // lanes per row
+    constexpr int R = kWave / G;   // rows per pass
+    constexpr int U = 8;           // passes in flight together
+    constexpr int PASSES = kWave / R;
+    const int lane = threadIdx.x % kWave;
+    const int sub = lane % G, rsub = lane / G;
+    const int32_t* idx = P.indices + static_cast<int64_t>(b) * P.tokens;
+    const float levels = static_cast<float>((1 << P.hat_bits) - 1);
+    const bool with = P.with_out != nullptr;
+    float c[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c[i] = centre[sub * 8 + i];
+    for (int m0 = begin + first; m0 < end; m0 += stride) {
+        const int cnt = min(kWave, end - m0);
+        const int mine = idx[m0 + min(lane, cnt - 1)];
+        for (int u0 = 0; u0 < PASSES && u0 * R < cnt; u0 += U) {
+            float xv[U][8];
+            Raw8<DT> wv[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int r = min((u0 + u) * R + rsub, cnt - 1);  // clamped: every load is unconditional
+                const int tok = __shfl(mine, r, kWave);
+                Row8<DT>::load(P.x, b * P.x_stride + static_cast<int64_t>(tok) * D + sub * 8, xv[u]);
+                if (with) wv[u].load(P.with_in, (static_cast<int64_t>(b) * P.length + tok) * D + sub * 8);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int r = (u0 + u) * R + rsub;
+                float out[8], lo, sc;
+                uint8_t q[8];
+                base_offset_lane<G>(xv[u], c, levels, out, q, lo, sc);
+                if (r < cnt) {
+                    const int64_t dst = (static_cast<int64_t>(b) * P.length + m0 + r) * D + sub * 8;
+                    Row8<DT>::store(P.hat, dst, out);
+                    if (with) wv[u].store(P.with_out, dst);
+                }
+            }
+        }
+    }
+}
+
+// Text rows [tokens, length) of every packed problem, copied into hat and with_out.
+template <int DT, int D>
+__device__ __forceinline__ void pack_text_rows(const KmArgs& a, int block) {
+    constexpr int G = D / 8;
+    const int sub = threadIdx.x % G;
+    const int nthreads = a.text_blocks * kUpdateWaves * kWave;
+    for (int p = 0; p < a.num; ++p) {
+        const KmProblem& P = a.p[p];
+        if (!P.hat) continue;
+        const int text = P.length - P.tokens;
+        const int64_t rows = static_cast<int64_t>(P.batch) * text;
+        for (int64_t r = (static_cast<int64_t>(block) * kUpdateWaves * kWave + threadIdx.x) / G; r < rows;
+             r += nthreads / G) {
+            const int64_t b = r / text;
+            const int t = P.tokens + static_cast<int>(r % text);
+            const int64_t dst = (b * P.length + t) * D + sub * 8;
+            Row8<DT>::copy(P.x, b * P.x_stride + static_cast<int64_t>(t) * D + sub * 8, P.hat, dst);
+            if (P.with_out) Row8<DT>::copy(P.with_in, dst, P.with_out, dst);
+        }
+    }
+}
+
+template <int DT, int D, bool kPack = false>
 __global__ __launch_bounds__(kUpdateWaves * kWave) void km_update_kernel(KmArgs a, KmIter it) {
     constexpr int PER = D / kWave;  // channels per lane (1 or 2)
     __shared__ float row[kUpdateWaves][D];
     __shared__ float carry[D];
+    if constexpr (kPack) {
+        if (static_cast<int>(blockIdx.x) >= a.total_upd_blocks) {
+            pack_text_rows<DT, D>(a, blockIdx.x - a.total_upd_blocks);
+            return;
+        }
+    }
     const int p = km_update_problem(a, blockIdx.x);
     const KmProblem& P = a.p[p];
     const int K = P.clusters;
@@ -826,7 +928,16 @@ __global__ __launch_bounds__(kUpdateWaves * kWave) void km_update_kernel(KmArgs 
             }
             for (int w = wave; w < kUpdateWaves; ++w) __syncthreads();
         }
-        if (wave != 0) return;
+        if (wave != 0) {
+            if constexpr (kPack) {
+                if (P.hat) {
+                    // The other wavefronts pack with wave 0 once it has left the centre in row[0].
+                    __syncthreads();
+                    pack_members<DT, D>(P, b, begin, end, row[0], kWave * wave, kWave * kUpdateWaves);
+                }
+            }
+            return;
+        }
         if (end > begin) {
 #pragma unroll
             for (int i = 0; i < PER; ++i) s[i] = carry[lane * PER + i];
@@ -850,6 +961,16 @@ __global__ __launch_bounds__(kUpdateWaves * kWave) void km_update_kernel(KmArgs 
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     if (lane == 0) P.norms[cl] = canonical_norm_lds(row[wave], D);
+    if constexpr (kPack) {
+        if (P.hat) {
+            if (shared) {
+                __syncthreads();  // row[0] (this wavefront's centre) is published to the others
+                pack_members<DT, D>(P, b, begin, end, row[0], 0, kWave * kUpdateWaves);
+            } else {
+                pack_members<DT, D>(P, b, begin, end, row[wave], 0, kWave);
+            }
+        }
+    }
 }
 
 constexpr int kScanWaves = 8;     // clusters per update workgroup (one per wavefront)
@@ -968,8 +1089,12 @@ hipError_t run_fit(KmArgs& a, const KmIter* iters, int iterations, SortArgs sa, 
         }
         hipError_t e = launch_cluster_sort(sa, s, false);
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL((km_update_kernel<DT, D>), dim3(a.total_upd_blocks), dim3(kUpdateWaves * kWave), 0, s, a,
-                           iters[i]);
+        if (i + 1 == iterations && a.text_blocks > 0)
+            hipLaunchKernelGGL((km_update_kernel<DT, D, true>), dim3(a.total_upd_blocks + a.text_blocks),
+                               dim3(kUpdateWaves * kWave), 0, s, a, iters[i]);
+        else
+            hipLaunchKernelGGL((km_update_kernel<DT, D>), dim3(a.total_upd_blocks), dim3(kUpdateWaves * kWave), 0, s,
+                               a, iters[i]);
     }
     return hipGetLastError();
 }
@@ -1002,6 +1127,11 @@ struct KmFitDesc {
     int32_t* indices;
     int32_t* offsets;
     int batch, tokens, clusters;
+    void* hat = nullptr;             // packing by the last update (see KmProblem)
+    const void* with_in = nullptr;
+    void* with_out = nullptr;
+    int hat_bits = 0;
+    int length = 0;
 };
 
 // Workspace (bytes) for one problem.
@@ -1067,6 +1197,17 @@ hipError_t km_fit(const KmFitDesc* descs, int num, int dims, int dtype, int iter
         P.upd_shared = d.tokens > 64 * d.clusters ? 1 : 0;
         P.upd_blocks = P.upd_shared ? d.batch * d.clusters
                                     : static_cast<int>(ceil_div(static_cast<int64_t>(d.batch) * d.clusters, kUpdateWaves));
+        P.hat = d.hat;
+        P.with_in = d.with_in;
+        P.with_out = d.with_out;
+        P.hat_bits = d.hat_bits;
+        P.length = d.length;
+        if (d.hat) {
+            // Text copies: one 16-byte chunk per thread and row, at most 64 workgroups.
+            const int64_t chunks = static_cast<int64_t>(d.batch) * std::max(d.length - d.tokens, 0) * (dims / 8);
+            a.text_blocks = std::max(a.text_blocks, static_cast<int>(std::min<int64_t>(
+                                                        64, std::max<int64_t>(1, ceil_div(chunks, kUpdateWaves * kWave)))));
+        }
         SortProblem& q = sa.p[i];
         q.labels = d.labels;
         q.indices = d.indices;
@@ -1163,6 +1304,47 @@ PECO_API int peco_kmeans_fit(int num_problems, const void* const* x, const int64
         d[i] = KmFitDesc{x[i], stride, centers_in[i], centers_out[i], labels[i], counts[i], sorted_indices[i],
                          offsets[i], batch[i], tokens[i], clusters[i]};
         if (!valid_fit(d[i]) || (stride != 0 && stride < static_cast<int64_t>(tokens[i]) * dims)) return kInvalidValue;
+        need += km_workspace_bytes(batch[i], tokens[i], clusters[i], dims);
+    }
+    if (workspace_bytes < need) return kWorkspaceTooSmall;
+    return km_fit(d, num_problems, dims, dtype, iterations, workspace, nullptr, static_cast<hipStream_t>(stream));
+}
+
+// peco_kmeans_fit whose last update also packs (fuses peco/processor.py:141-149 for the
+// problems given a hat): problem i with hat[i] writes hat[i] [batch, length, dims] (rows
+// [0, tokens) = x's rows in the final cluster order, Base-Offset fake-quantized with bits[i]
+// against the final centres; rows [tokens, length) = x's rows there, so x_batch_stride[i]
+// must cover length rows), and with_in[i] -> with_out[i] ([batch, length, dims], nullable)
+// gathered in the same order with its text rows copied.
+PECO_API int peco_kmeans_fit_pack(int num_problems, const void* const* x, const int64_t* x_batch_stride,
+                                  const float* const* centers_in, float* const* centers_out, int32_t* const* labels,
+                                  int32_t* const* counts, int32_t* const* sorted_indices, int32_t* const* offsets,
+                                  const int* batch, const int* tokens, const int* clusters, int dims, int dtype,
+                                  int iterations, void* const* hat, const int* bits, const void* const* with_in,
+                                  void* const* with_out, int length, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+    if (num_problems < 1 || num_problems > kMaxKm || iterations < 1 || (dims != 64 && dims != 128) ||
+        (dtype != kBF16 && dtype != kF16 && dtype != kF32) || !workspace || !hat || !bits || !with_in || !with_out)
+        return kInvalidValue;
+    KmFitDesc d[kMaxKm];
+    size_t need = 0;
+    for (int i = 0; i < num_problems; ++i) {
+        const int64_t stride = x_batch_stride ? x_batch_stride[i] : 0;
+        d[i] = KmFitDesc{x[i], stride, centers_in[i], centers_out[i], labels[i], counts[i], sorted_indices[i],
+                         offsets[i], batch[i], tokens[i], clusters[i]};
+        if (!valid_fit(d[i]) || (stride != 0 && stride < static_cast<int64_t>(tokens[i]) * dims)) return kInvalidValue;
+        if (hat[i]) {
+            if ((bits[i] != 4 && bits[i] != 8) || length < tokens[i] ||
+                (length > tokens[i] && stride < static_cast<int64_t>(length) * dims) || (!with_in[i] != !with_out[i]))
+                return kInvalidValue;
+            d[i].hat = hat[i];
+            d[i].hat_bits = bits[i];
+            d[i].with_in = with_in[i];
+            d[i].with_out = with_out[i];
+            d[i].length = length;
+        } else if (with_in[i] || with_out[i]) {
+            return kInvalidValue;
+        }
         need += km_workspace_bytes(batch[i], tokens[i], clusters[i], dims);
     }
     if (workspace_bytes < need) return kWorkspaceTooSmall;

@@ -2,115 +2,19 @@
 // plus the fused "pack" kernel that applies it while gathering Q/K/V into cluster order
 // and appending the unsorted text rows (peco/processor.py:141-149).
 //
-// Per token, over all D channels, in this fp32 order (one rounding per line):
-//   r = x - C[label]; low = min r; high = max r
-//   scale = (high - low) / (2^bits - 1), or 1 when not positive
-//   code  = clamp(rint((r - low) / scale), 0, 2^bits - 1)      (rint = half-to-even)
-//   xhat  = C[label] + (low + scale * code), cast to the input dtype (RNE)
-// The translation unit is built with -ffp-contract=off and correctly rounded division,
-// so every line above is one IEEE operation, as in the torch reference.
+// The per-token arithmetic (base_offset.hpp) is one IEEE operation per step, in the torch
+// reference's order.
 //
 // Layout: a token row of D elements is handled by G = D/8 lanes (8 elements per lane,
 // 16-byte loads for 16-bit inputs), so one wavefront covers 64/G rows and min/max are
 // reduced with log2(G) xor-shuffles inside the lane group. HBM-bound streaming kernel.
+#include "base_offset.hpp"
 #include "common.hpp"
 
 #include <algorithm>
 
 namespace peco {
 namespace {
-
-template <int DT> struct Row8 {
-    // Loads 8 consecutive elements (starting at element offset e) as fp32.
-    __device__ __forceinline__ static void load(const void* base, int64_t e, float (&v)[8]) {
-        if constexpr (DT == kF32) {
-            const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(base) + e);
-            const f32x4 a = p[0], b = p[1];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) { v[i] = a[i]; v[4 + i] = b[i]; }
-        } else {
-            const u16x8 u = *reinterpret_cast<const u16x8*>(static_cast<const uint16_t*>(base) + e);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = half_to_f32<DT>(u[i]);
-        }
-    }
-    __device__ __forceinline__ static void store(void* base, int64_t e, const float (&v)[8]) {
-        if constexpr (DT == kF32) {
-            f32x4* p = reinterpret_cast<f32x4*>(static_cast<float*>(base) + e);
-            p[0] = f32x4{v[0], v[1], v[2], v[3]};
-            p[1] = f32x4{v[4], v[5], v[6], v[7]};
-        } else {
-            u16x8 u;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) u[i] = f32_to_half<DT>(v[i]);
-            *reinterpret_cast<u16x8*>(static_cast<uint16_t*>(base) + e) = u;
-        }
-    }
-    // Bit-exact copy of 8 elements.
-    __device__ __forceinline__ static void copy(const void* src, int64_t es, void* dst, int64_t ed) {
-        if constexpr (DT == kF32) {
-            const u32x4* p = reinterpret_cast<const u32x4*>(static_cast<const float*>(src) + es);
-            u32x4* q = reinterpret_cast<u32x4*>(static_cast<float*>(dst) + ed);
-            q[0] = p[0];
-            q[1] = p[1];
-        } else {
-            *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(dst) + ed) =
-                *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(src) + es);
-        }
-    }
-};
-
-__device__ __forceinline__ void load_centroid8(const float* c, float (&v)[8]) {
-    const f32x4 a = reinterpret_cast<const f32x4*>(c)[0];
-    const f32x4 b = reinterpret_cast<const f32x4*>(c)[1];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) { v[i] = a[i]; v[4 + i] = b[i]; }
-}
-
-// Quantize 8 residual channels of one token held by this lane; the lane group of G lanes
-// together holds the whole token. Returns codes, writes xhat, low and scale.
-template <int G>
-__device__ __forceinline__ void base_offset_lane(const float (&x)[8], const float (&c)[8], float levels,
-                                                 float (&xhat)[8], uint8_t (&code)[8], float& low_out,
-                                                 float& scale_out) {
-    float r[8];
-    float lo = INFINITY, hi = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        r[i] = x[i] - c[i];
-        lo = fminf(lo, r[i]);
-        hi = fmaxf(hi, r[i]);
-    }
-#pragma unroll
-    for (int m = 1; m < G; m <<= 1) {
-        lo = fminf(lo, __shfl_xor(lo, m, G));
-        hi = fmaxf(hi, __shfl_xor(hi, m, G));
-    }
-    const float span = hi - lo;
-    const float raw = span / levels;
-    const float scale = raw > 0.0f ? raw : 1.0f;
-    // code = rint(RN(shifted / scale)) with the division done once per row: qa = shifted * inv
-    // (inv = RN(1 / scale)) and Q = shifted / scale satisfy |qa - Q| <= Q * (2^-23 + 2^-48),
-    // and |RN(Q) - Q| <= Q * 2^-24 with Q <= levels, so rint(qa) == rint(RN(Q)) unless qa lies
-    // within levels * 1.8e-7 of a half-integer. There (tol = levels * 2^-21 with margin; the
-    // distance qa - rint(qa) is computed exactly) the correctly rounded division decides.
-    const float inv = 1.0f / scale;
-    const float tol = levels * 4.76837158203125e-7f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float shifted = r[i] - lo;
-        const float qa = shifted * inv;
-        float q = __builtin_rintf(qa);
-        if (fabsf(qa - q) >= 0.5f - tol) q = __builtin_rintf(shifted / scale);
-        q = q < 0.0f ? 0.0f : (q > levels ? levels : q);
-        code[i] = static_cast<uint8_t>(q);
-        const float step = scale * static_cast<float>(code[i]);
-        const float resid = lo + step;
-        xhat[i] = c[i] + resid;
-    }
-    low_out = lo;
-    scale_out = scale;
-}
 
 template <int DT, int G>
 __global__ __launch_bounds__(256) void base_offset_kernel(const void* __restrict__ x, const int32_t* __restrict__ labels,

@@ -137,16 +137,21 @@ class PecoAttention:
         self.q_centroids = None
         self.k_centroids = None
         self._last_fit = None
+        self._last_pack = None
 
     def reset(self):
         self.q_centroids = self.k_centroids = None
         self._last_fit = None
+        self._last_pack = None
 
-    def _update_cluster_state(self, query, key):
+    def _update_cluster_state(self, query, key, pack_keys=None):
         """Fit Q/K partitions, reusing this layer's centres after initialization.
 
         query/key are the video parts [B,H,N,D]; returns (q_labels, k_labels, q_sizes, k_sizes)
-        with sizes [B,H,K]. Both fits run in the same launches.
+        with sizes [B,H,K]. Both fits run in the same launches. With ``pack_keys = (bits,
+        key_full, value_full)`` ([B,H,S,D], key the tensor whose video part is ``key``) the
+        last update also writes K Base-Offset fake-quantized and V, both in the final key
+        cluster order with the text rows after them, into ``self._last_pack``.
         """
         batch, heads, length, dim = query.shape
         initializing = self.q_centroids is None
@@ -163,9 +168,24 @@ class PecoAttention:
         k_init = self._initial_centers(k_flat, self.k_centroids, self.config.num_k_centroids)
         if q_flat.dtype not in (torch.float16, torch.bfloat16, torch.float32) or q_flat.dtype != k_flat.dtype:
             q_flat, k_flat = q_flat.float(), k_flat.float()
-        (q_labels, q_cent, q_sizes, q_idx, _), (k_labels, k_cent, k_sizes, k_idx, _) = clustering_cuda.kmeans_fit(
-            [clustering_cuda.KMeansProblem(q_flat, q_init), clustering_cuda.KMeansProblem(k_flat, k_init)],
-            iterations)
+        self._last_pack = None
+        if pack_keys is None:
+            problems = [clustering_cuda.KMeansProblem(q_flat, q_init), clustering_cuda.KMeansProblem(k_flat, k_init)]
+            outs = clustering_cuda.kmeans_fit(problems, iterations)
+        else:
+            # The key rows are fitted in place in the full [B*H, S, D] tensor, whose rows past
+            # the video part (the text) the packing copies.
+            bits, key_full, value_full = pack_keys
+            full = key_full.shape[2]
+            if key_full.dtype != k_flat.dtype or not key_full.is_contiguous() or not value_full.is_contiguous():
+                raise ValueError("the packed key and value must be contiguous [B,H,S,D] tensors like key")
+            k_rows = key_full.reshape(batch * heads, full, dim)[:, :length]
+            value_flat = value_full.reshape(batch * heads, full, dim)
+            problems = [clustering_cuda.KMeansProblem(q_flat, q_init), clustering_cuda.KMeansProblem(k_rows, k_init)]
+            outs, packed = clustering_cuda.kmeans_fit(problems, iterations, pack=[None, (bits, full, value_flat)])
+            k_hat, v_perm = packed[1]
+            self._last_pack = (k_hat.view(batch, heads, full, dim), v_perm.view(batch, heads, full, dim))
+        (q_labels, q_cent, q_sizes, q_idx, _), (k_labels, k_cent, k_sizes, k_idx, _) = outs
         self.q_centroids, self.k_centroids = q_cent, k_cent
         self._last_fit = (q_idx, k_idx)
         return q_labels, k_labels, q_sizes.reshape(batch, heads, -1), k_sizes.reshape(batch, heads, -1)
@@ -203,8 +223,10 @@ class PecoAttention:
         bits = self.config.base_offset_bits
         _validate_bits(bits, allow_bypass=True)
         query, key, value = query.contiguous(), key.contiguous(), value.contiguous()
+        # With Base-Offset on, the last k-means update also writes K fake-quantized and V in
+        # key-cluster order (stages 2-3 of K/V fused into the fit).
         q_labels, k_labels, q_sizes, k_sizes = self._update_cluster_state(
-            query[:, :, :video_length], key[:, :, :video_length])
+            query[:, :, :video_length], key[:, :, :video_length], pack_keys=(bits, key, value) if bits else None)
         q_idx, k_idx = self._last_fit
         # Cluster connectivity from the floating-point centres, extended with the text
         # partition (select_cluster_connections + extend_text_partition), in one launch that
@@ -219,12 +241,12 @@ class PecoAttention:
             # writes the output in original order, so no packed copy is made.
             return sparse_attention_work(query, key, value, work, out_index=q_idx, out_index_rows=video_length,
                                          k_index=k_idx)
-        # Fake-quantize Q/K against their centroids while packing Q/K/V into cluster order.
-        q_perm, k_perm, v_perm = clustering_cuda.pack_clustered(
-            [query, key, value], [q_idx, k_idx, k_idx], [q_labels, k_labels, None],
-            [self.q_centroids, self.k_centroids, None], [bits, bits, 0], video_length)
-        # Video rows return to their original positions; text rows keep theirs.
-        return sparse_attention_work(q_perm, k_perm, v_perm, work, out_index=q_idx, out_index_rows=video_length)
+        # K (fake-quantized) and V come packed from the fit; Q is read in its original order
+        # through the permutation and fake-quantized as the attention loads it. Video rows
+        # return to their original positions; text rows keep theirs.
+        k_perm, v_perm = self._last_pack
+        return sparse_attention_work(query, k_perm, v_perm, work, out_index=q_idx, out_index_rows=video_length,
+                                     q_centroids=self.q_centroids, bits=bits)
 
     @torch.no_grad()
     def __call__(self, attn, hidden_states, encoder_hidden_states=None, attention_mask=None, image_rotary_emb=None):

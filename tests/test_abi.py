@@ -63,5 +63,16 @@ def test_work_list_entries_reject_bad_arguments_and_size_the_buffer():
     assert lib.peco_select_work_size(0, 7006, 64, 256, 1) == 0
     assert lib.peco_select_work(null, null, null, null, 1, 4, 4, 128, 0.5, 0, 0, 0, 0, 16, 16, null, null, null,
                                 null, 1 << 20, null) == 1
-    assert lib.peco_sparse_attention_work(null, null, null, null, null, 0, null, null, 0, 1, 16, 16, 128, 4, 4, 1,
-                                          null) == 1
+    assert lib.peco_sparse_attention_work(null, null, null, null, null, 0, null, null, 0, 0, null, 0, 1, 16, 16, 128,
+                                          4, 4, 1, null) == 1
+
+
+def test_library_leaves_no_own_symbol_undefined():
+    """A kernel whose host stub was not emitted leaves an undefined symbol that only fails at
+    load time on the GPU host; catch it here."""
+    if not _native.LIB_PATH.exists():
+        _native.build_library()
+    out = subprocess.run(["nm", "-D", "--undefined-only", str(_native.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    own = [line for line in out.splitlines() if "peco" in line]
+    assert not own, f"undefined symbols of the library's own code: {own}"
