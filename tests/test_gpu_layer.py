@@ -238,3 +238,58 @@ def test_layer_full_length_720p_head_matches_oracle(announce):
     print(f"[720p head] max {err.max().item():.3e} mean {err.mean().item():.3e}", flush=True)
     assert err.mean().item() <= 2e-3
     assert err.max().item() <= 2e-2
+
+
+def test_layer_544p_zipf_sequence_full_length_matches_oracle(announce):
+    """The 10-call denoising sequence of the Zipf workload on one head at its full length
+    (32640 video + 256 text tokens, 128/512 clusters, 20% kept, Base-Offset 4-bit): the first
+    call fits 10 iterations from the seeded centroids, every later call warm-starts from the
+    previous call's centroids with 3 iterations on Q/K drifted by N(0, 0.1^2) per step, as the
+    bench's sequence does. Every call's permutations and centroids are bit-exact against the C
+    oracle started from the oracle's own previous centroids, and its output is compared with
+    the oracle's layer (fp32 torch block-sparse attention on the CPU)."""
+    wl = workloads.make_workload("hunyuan_544p_zipf", heads=1)
+    shape = wl.shape
+    n = shape.video
+    announce(f"544p Zipf sequence: heads=1 video={n} calls={shape.steps} init={shape.iterations} "
+             f"warm={shape.warm_iterations}")
+    cfg = processor.PecoConfig(num_q_centroids=shape.num_q_centroids, num_k_centroids=shape.num_k_centroids,
+                               top_p=wl.top_p, min_kc_ratio=wl.min_kc_ratio, kmeans_iter_init=shape.iterations,
+                               kmeans_iter_step=shape.iterations, warmup_steps=0, base_offset_bits=shape.bits)
+    ctx = processor.InferenceContext(step=0, text_length=shape.text, valid_text_length=shape.text)
+    layer = processor.PecoAttention(0, cfg, ctx)
+    layer.q_centroids, layer.k_centroids = wl.q_init.to(DEV), wl.k_init.to(DEV)
+    q_init, k_init = wl.q_init, wl.k_init
+    worst = 0.0
+    for step in range(shape.steps):
+        iters = shape.iterations if step == 0 else shape.warm_iterations
+        layer.config = processor.PecoConfig(**{**cfg.__dict__, "kmeans_iter_step": iters})
+        cur = wl if step == 0 else workloads.drift(wl, step)
+        print(f"[case] call {step}: {iters} iterations", flush=True)
+        with torch.no_grad():
+            out = layer.attention(cur.query.to(DEV), cur.key.to(DEV), cur.value.to(DEV))
+        torch.cuda.synchronize()
+        fits = {}
+        for name, x, init in (("q", cur.query, q_init), ("k", cur.key, k_init)):
+            fits[name] = canonical.kmeans_fit(x[0, :, :n].float().numpy(), init.numpy(), iters)
+        q_idx, k_idx = (t.cpu().numpy() for t in layer._last_fit)
+        assert np.array_equal(q_idx, fits["q"][3]), f"call {step}: Q permutation"
+        assert np.array_equal(k_idx, fits["k"][3]), f"call {step}: K permutation"
+        assert np.array_equal(layer.q_centroids.cpu().numpy().view(np.int32), fits["q"][1].view(np.int32))
+        assert np.array_equal(layer.k_centroids.cpu().numpy().view(np.int32), fits["k"][1].view(np.int32))
+
+        def fit(x, clusters, iterations, init, fits=fits):
+            labels, centers, counts, _, _ = fits["q" if clusters == shape.num_q_centroids else "k"]
+            return torch.from_numpy(labels), torch.from_numpy(centers), torch.from_numpy(counts), iterations
+
+        ref = reference_path.peco_layer(
+            cur.query, cur.key, cur.value, num_q_centroids=shape.num_q_centroids,
+            num_k_centroids=shape.num_k_centroids, iterations=iters, q_init=q_init, k_init=k_init, top_p=wl.top_p,
+            min_kc_ratio=wl.min_kc_ratio, bits=shape.bits, text_length=shape.text, valid_text=shape.text, fit=fit)
+        err = (out.float().cpu() - ref.float()).abs()
+        print(f"[544p sequence] call {step}: max {err.max().item():.3e} mean {err.mean().item():.3e}", flush=True)
+        assert err.mean().item() <= 2e-3
+        assert err.max().item() <= 2e-2
+        worst = max(worst, err.max().item())
+        q_init, k_init = torch.from_numpy(fits["q"][1]), torch.from_numpy(fits["k"][1])
+    print(f"[544p sequence] worst max error over {shape.steps} calls: {worst:.3e}", flush=True)
