@@ -89,14 +89,18 @@ int peco_kmeans_fit(int num_problems, const void* const* x, const int64_t* x_bat
  * in the final cluster order, Base-Offset fake-quantized with bits[i] (4 or 8) against the
  * final centres, then x's rows [tokens, length) unchanged (the text; x_batch_stride[i] must
  * cover length rows); with_in[i] -> with_out[i] ([batch, length, dims], both or neither)
- * are gathered in the same order with their text rows copied. Labels, centres, counts and
- * the permutation are those of peco_kmeans_fit. (ABI revision 3.) */
+ * are gathered in the same order with their text rows copied. codes[i], low[i], scale[i]
+ * (all three or none; uint8 [batch, tokens, dims], fp32 [batch, tokens]) receive the
+ * Base-Offset payload of hat[i]'s first tokens rows in the same order, as
+ * quantize_base_offset computes it (peco/quantization.py:97-128). Labels, centres, counts and
+ * the permutation are those of peco_kmeans_fit. (ABI revision 4: codes/low/scale added.) */
 int peco_kmeans_fit_pack(int num_problems, const void* const* x, const int64_t* x_batch_stride,
                          const float* const* centers_in, float* const* centers_out, int32_t* const* labels,
                          int32_t* const* counts, int32_t* const* sorted_indices, int32_t* const* offsets,
                          const int* batch, const int* tokens, const int* clusters, int dims, int dtype, int iterations,
                          void* const* hat, const int* bits, const void* const* with_in, void* const* with_out,
-                         int length, void* workspace, size_t workspace_bytes, void* stream);
+                         uint8_t* const* codes, float* const* low, float* const* scale, int length,
+                         void* workspace, size_t workspace_bytes, void* stream);
 
 /* Diagnostic of the certified assignment (no counterpart in the reference): for bf16 x
  * [batch, tokens, dims] and fp32 centres, screened[b,t,j] receives the MFMA screen value
@@ -169,6 +173,9 @@ int peco_select_cluster_connections(const float* qc, const float* kc, const int3
 /* ABI revision 3 added peco_select_work_size, peco_select_work, peco_sparse_attention_work
  * and peco_kmeans_fit_pack. */
 
+/* ABI revision 4 added peco_base_offset_attention and the codes/low/scale outputs of
+ * peco_kmeans_fit_pack. */
+
 /* int32 elements of peco_select_work's work buffer (bh entries, sq query rows, a cq(+2) x
  * ck(+2) map). */
 size_t peco_select_work_size(int bh, int sq, int cq, int ck, int extend);
@@ -203,6 +210,28 @@ int peco_sparse_attention_work(const void* q, const void* k, const void* v, void
                                int out_index_rows, const int32_t* k_index, const float* q_centroids, int q_clusters,
                                int bits, const int32_t* work, size_t work_ints, int bh, int sq, int sk, int d, int cq,
                                int ck, int dtype, void* stream);
+
+/* Cluster-sparse attention with Base-Offset scores on the integer MFMA. No counterpart in the
+ * reference, which reconstructs Q/K and runs floating-point attention (peco/quantization.py:
+ * 1-22 gives the four-term expansion it leaves unused; README.md:18). Map-driven like
+ * peco_sparse_attention_ex (selected, q_sizes, k_sizes of the map extended with the text
+ * partition, workspace of peco_sparse_attention_workspace_size). q is in original token order:
+ * video row j < oi_rows of the cluster order is read from row out_index[j] (which also places
+ * its output row) and Base-Offset quantized with `bits` (4 or 8) against q_centroids [bh, kq,
+ * d]. k (video rows fake-quantized), v, k_codes uint8 [bh, oi_rows, d], k_low and k_scale fp32
+ * [bh, oi_rows] are in key cluster order, as peco_kmeans_fit_pack writes them. The key
+ * centroids enter as three int8 planes kc_planes [bh, kk, 3, d] with kc_scale [bh, kk]
+ * (centroid = kc_scale * (P0 + P1/128 + P2/16384)), their sums kc_sum [bh, kk] and
+ * qk_dot [bh, kk, kq] = Ck.Cq. Video x video scores are the exact expansion of
+ * (Cq + a + s u).(Ck + b + t w) with u.w from v_mfma_i32_32x32x32_i8; scores involving text
+ * rows use the fake-quantized rows on bf16/fp16 MFMA, as the reference does. */
+int peco_base_offset_attention(const void* q, const int32_t* out_index, const float* q_centroids, int kq,
+                               const void* k, const void* v, const uint8_t* k_codes, const float* k_low,
+                               const float* k_scale, const int8_t* kc_planes, const float* kc_scale,
+                               const float* kc_sum, const float* qk_dot, int kk, int bits, const uint8_t* selected,
+                               const int* q_sizes, const int* k_sizes, void* output, int* workspace,
+                               size_t workspace_ints, int bh, int sq, int sk, int oi_rows, int d, int cq, int ck,
+                               int dtype, void* stream);
 
 /* peco_sparse_attention without a workspace argument. No counterpart in the reference: it is
  * for callers that cannot allocate device memory (code under HIP graph capture, serving loops

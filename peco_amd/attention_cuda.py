@@ -242,3 +242,111 @@ def sparse_attention_work(
             message = library.peco_attention_error_string(error).decode("utf-8", errors="replace")
             raise RuntimeError(f"PECO HIP sparse attention launch failed: {message} ({error})")
     return output
+
+
+def centroid_planes(centroids: torch.Tensor):
+    """Key centroids [BH, K, D] fp32 as three int8 planes and a scale per centroid:
+    C = cs * (P0 + P1/128 + P2/16384) to within 2^-22 * max|C| of each centroid, plus Sum(C).
+
+    Returns (planes int8 [BH, K, 3, D], cs fp32 [BH, K], sums fp32 [BH, K]). cs = max|C|/127
+    (1 for a zero centroid); each plane is the rounded remainder of the one before, scaled
+    by 128.
+    """
+    c = centroids.float()
+    cs = c.abs().amax(dim=-1) / 127.0
+    cs = torch.where(cs > 0, cs, torch.ones_like(cs))
+    x = c / cs[..., None]
+    p0 = torch.round(x).clamp_(-127, 127)
+    r1 = (x - p0) * 128.0
+    p1 = torch.round(r1).clamp_(-127, 127)
+    r2 = (r1 - p1) * 128.0
+    p2 = torch.round(r2).clamp_(-127, 127)
+    planes = torch.stack((p0, p1, p2), dim=-2).to(torch.int8).contiguous()
+    return planes, cs.contiguous(), c.sum(dim=-1).contiguous()
+
+
+def base_offset_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    dynamic_map: torch.Tensor,
+    q_sizes: torch.Tensor,
+    k_sizes: torch.Tensor,
+    *,
+    out_index: torch.Tensor,
+    q_centroids: torch.Tensor,
+    k_centroids: torch.Tensor,
+    k_codes: torch.Tensor,
+    k_low: torch.Tensor,
+    k_scale: torch.Tensor,
+    bits: int,
+) -> torch.Tensor:
+    """Cluster-sparse attention with Base-Offset scores on the integer MFMA (an extension: the
+    reference reconstructs Q/K and runs floating-point attention, peco/quantization.py:1-22,
+    README.md:18).
+
+    Video query rows against video key clusters score through the exact expansion of
+    (Cq + a + s u).(Ck + b + t w) with u.w on v_mfma_i32_32x32x32_i8; text scores use the
+    fake-quantized bf16 rows as the reference does. Inputs: ``q`` [B,H,S,D] in original
+    order (its first N = ``out_index.shape[-1]`` video rows Base-Offset quantized at load
+    against ``q_centroids`` [B*H, KQ, D], rows j < N of the cluster order read from
+    ``out_index[j]``, which also places the output); ``k`` (video rows fake-quantized), ``v``
+    [B,H,S,D] and ``k_codes`` uint8 [B*H, N, D], ``k_low``/``k_scale`` fp32 [B*H, N] in key
+    cluster order, as ``clustering_cuda.kmeans_fit`` packs them (``k_centroids`` [B*H, KK, D]);
+    the extended map [B,H,KQ+2,KK+2] and sizes of ``clustering_cuda.select_connections`` with
+    the text partition.
+    """
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not isinstance(t, torch.Tensor) or not t.is_cuda or not t.is_contiguous() or t.dim() != 4:
+            raise ValueError(f"{name} must be a contiguous 4-D GPU tensor")
+    if q.dtype not in (torch.float16, torch.bfloat16) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("PECO HIP sparse attention supports float16 and bfloat16")
+    batch, heads, sq, dim = q.shape
+    sk = k.shape[2]
+    bh = batch * heads
+    if k.shape != (batch, heads, sk, dim) or v.shape != k.shape or dim not in (64, 128):
+        raise ValueError("q/k/v shapes must be [B,H,S,D] with D in {64, 128} and matching K/V")
+    if bits not in (4, 8):
+        raise ValueError("bits must be 4 or 8")
+    if dynamic_map.dtype != torch.bool or dynamic_map.dim() != 4 or dynamic_map.shape[:2] != (batch, heads):
+        raise ValueError("dynamic_map must be bool [B,H,CQ,CK]")
+    cq, ck = dynamic_map.shape[2:]
+    if tuple(q_sizes.shape) != (batch, heads, cq) or tuple(k_sizes.shape) != (batch, heads, ck):
+        raise ValueError("q_sizes/k_sizes must be [B,H,CQ] and [B,H,CK]")
+    rows = out_index.shape[-1]
+    _check_index(out_index, "out_index", batch, heads, rows)
+    if not 1 <= rows <= min(sq, sk):
+        raise ValueError("out_index must cover between 1 and min(SQ, SK) video rows")
+    kq, kk = q_centroids.shape[1], k_centroids.shape[1]
+    for name, t, shape in (("q_centroids", q_centroids, (bh, kq, dim)), ("k_centroids", k_centroids, (bh, kk, dim)),
+                           ("k_low", k_low, (bh, rows)), ("k_scale", k_scale, (bh, rows))):
+        if t.dtype != torch.float32 or not t.is_contiguous() or tuple(t.shape) != shape or t.device != q.device:
+            raise ValueError(f"{name} must be contiguous fp32 {list(shape)} on the device of q")
+    if k_codes.dtype != torch.uint8 or not k_codes.is_contiguous() or tuple(k_codes.shape) != (bh, rows, dim):
+        raise ValueError("k_codes must be contiguous uint8 [B*H, N, D]")
+    if not 1 <= kq <= cq or not 1 <= kk <= ck:
+        raise ValueError("the centroids must describe the first clusters of the map")
+    output = torch.empty_like(q)
+    with torch.cuda.device(q.device):
+        if not _device_is_gfx950(q.device):
+            raise RuntimeError("This HIP build requires an MI355X-class gfx950 GPU")
+        library = _native.library()
+        planes, cs, csum = centroid_planes(k_centroids)
+        qk_dot = torch.bmm(k_centroids.double(), q_centroids.double().transpose(1, 2).contiguous()).float()
+        smap = dynamic_map.contiguous().view(torch.uint8)
+        qs = q_sizes.to(torch.int32).contiguous()
+        ks = k_sizes.to(torch.int32).contiguous()
+        ws_ints = library.peco_sparse_attention_workspace_size(bh, sq, sk, cq, ck)
+        workspace = torch.empty(ws_ints, dtype=torch.int32, device=q.device)
+        stream = _native.current_stream(q.device, q, k, v, output, out_index, q_centroids, k_codes, k_low, k_scale,
+                                        planes, cs, csum, qk_dot, smap, qs, ks, workspace)
+        error = library.peco_base_offset_attention(
+            _native.ptr(q), _native.ptr(out_index), _native.ptr(q_centroids), kq, _native.ptr(k), _native.ptr(v),
+            _native.ptr(k_codes), _native.ptr(k_low), _native.ptr(k_scale), _native.ptr(planes), _native.ptr(cs),
+            _native.ptr(csum), _native.ptr(qk_dot), kk, int(bits), _native.ptr(smap), _native.ptr(qs),
+            _native.ptr(ks), _native.ptr(output), _native.ptr(workspace), ws_ints, bh, sq, sk, rows, dim, cq, ck,
+            0 if q.dtype == torch.float16 else 1, stream)
+        if error:
+            message = library.peco_attention_error_string(error).decode("utf-8", errors="replace")
+            raise RuntimeError(f"PECO HIP Base-Offset attention launch failed: {message} ({error})")
+    return output

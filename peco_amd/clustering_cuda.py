@@ -141,7 +141,10 @@ def kmeans_fit(problems, iterations, pack=None):
     fake-quantized with ``bits`` against the final centres, then x's rows [N, length) (the
     text, which x's batch stride must cover); ``with_tensor`` ([B, length, D] or None) is
     gathered in the same order into a new tensor. Then returns (outs, packed) with packed[i] =
-    (hat, with_out) or None.
+    (hat, with_out) or None. An entry ``(bits, length, with_tensor, True)`` also returns the
+    Base-Offset payload of hat's first N rows in that order: packed[i] = (hat, with_out,
+    codes uint8 [B, N, D], low fp32 [B, N], scale fp32 [B, N]), the values
+    quantize_base_offset computes (peco/quantization.py:97-128).
     """
     library = _library()
     if not 1 <= len(problems) <= 2:
@@ -184,12 +187,14 @@ def kmeans_fit(problems, iterations, pack=None):
         _raise_cluster_error(status)
         return outs
     length = None
-    hats, withs_in, withs_out, bits = [], [], [], []
+    hats, withs_in, withs_out, bits, payloads = [], [], [], [], []
     for p, spec in zip(problems, pack):
         if spec is None:
             hats.append(None), withs_in.append(None), withs_out.append(None), bits.append(0)
+            payloads.append(None)
             continue
-        b, n, w = spec
+        b, n, w = spec[:3]
+        want_codes = len(spec) > 3 and bool(spec[3])
         if length is not None and n != length:
             raise ValueError("packed problems must share one length")
         length = int(n)
@@ -204,13 +209,20 @@ def kmeans_fit(problems, iterations, pack=None):
             withs_out.append(None)
         withs_in.append(w)
         bits.append(int(b))
+        payloads.append((torch.empty((p.batch, p.tokens, dims), dtype=torch.uint8, device=dev),
+                         torch.empty((p.batch, p.tokens), dtype=torch.float32, device=dev),
+                         torch.empty((p.batch, p.tokens), dtype=torch.float32, device=dev)) if want_codes else None)
+    codes, lows, scales = ([None if q is None else q[i] for q in payloads] for i in range(3))
+    extra = [t for t in hats + withs_in + withs_out + codes + lows + scales if t is not None]
     with torch.cuda.device(dev):
         status = library.peco_kmeans_fit_pack(
             *common, _native.ptr_array(hats), _native.int_array(bits), _native.ptr_array(withs_in),
-            _native.ptr_array(withs_out), int(length or 0), _native.ptr(ws), ws_bytes,
-            _retain_on_current_stream(dev, *tensors, *[t for t in hats + withs_in + withs_out if t is not None]))
+            _native.ptr_array(withs_out), _native.ptr_array(codes), _native.ptr_array(lows),
+            _native.ptr_array(scales), int(length or 0), _native.ptr(ws), ws_bytes,
+            _retain_on_current_stream(dev, *tensors, *extra))
     _raise_cluster_error(status)
-    packed = [None if h is None else (h, w) for h, w in zip(hats, withs_out)]
+    packed = [None if h is None else ((h, w) if q is None else (h, w, *q))
+              for h, w, q in zip(hats, withs_out, payloads)]
     return outs, packed
 
 

@@ -750,6 +750,443 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
         }
 }
 
+// ---- Base-Offset scores on the integer MFMA (an extension: the reference runs no such kernel,
+// README.md:18) ----
+//
+// With Base-Offset on, a video query row is q^ = Cq + a + s*u and a video key row
+// k^ = Ck + b + t*w (u, w the codes, a, b the row lows, s, t the row scales, Cq, Ck the
+// centroids of the row's cluster; peco/quantization.py:13-22 gives this form and the four-term
+// expansion). Their dot product is, exactly,
+//   q^.k^ = Cq.k^ + a*Sum(k^) + s*(u.Ck + b*Sum(u) + t*(u.w)),
+//   Cq.k^ = Cq.Ck + b*Sum(Cq) + t*(Cq.w),   Sum(k^) = Sum(Ck) + D*b + t*Sum(w).
+// 8-bit codes are moved to int8 by subtracting 128 (a and b then absorb 128s and 128t).
+// - u.w, the only term over query row x key, is exact int32 from v_mfma_i32_32x32x32_i8
+//   (half the MFMA issue of the bf16 S^T).
+// - u.Ck (query row x key cluster) also runs on the integer MFMA, against the key centroids
+//   held as three int8 planes, Ck = cs*(P0 + P1/128 + P2/16384) to within 2^-22 |Ck|max,
+//   for 32 kept clusters at a time, into an LDS table per wavefront.
+// - Cq.w and Sum(w) are reduced per key from its codes while the tile is staged; Cq.Ck and
+//   Sum(Ck) come per tile, Sum(u), a and s per row.
+// Scores of video rows against text keys, and every score of a text row (text is not
+// quantized, peco/processor.py:141-142), use bf16 MFMA on the fake-quantized rows, as the
+// reference computes all of them. The key stream is walked one kept key cluster at a time,
+// in tiles of 32 keys (the reference's own tile, peco/kernels/sparse_attention.cu:99-107), so a
+// tile has one key centroid. The scores are those of unrounded q^, k^ (the reference rounds
+// them to the input dtype before its attention, peco/quantization.py:136).
+struct BoAttnArgs {
+    const uint16_t* q;         // [bh, sq, D], original token order
+    const int32_t* out_index;  // [bh, oi_rows]: cluster-order query row -> original row
+    const float* q_cent;       // [bh, kq, D]
+    const uint16_t* k;         // [bh, sk, D], cluster order: video rows fake-quantized, text rows raw
+    const uint16_t* v;         // [bh, sk, D], cluster order
+    const uint8_t* k_codes;    // [bh, oi_rows, D], cluster order
+    const float* k_low;        // [bh, oi_rows]
+    const float* k_scale;      // [bh, oi_rows]
+    const int8_t* kc_planes;   // [bh, kk, 3, D]
+    const float* kc_scale;     // [bh, kk]
+    const float* kc_sum;       // [bh, kk]: Sum(Ck)
+    const float* qk_dot;       // [bh, kk, kq]: Ck.Cq
+    const uint8_t* selected;   // [bh, cq, ck]
+    const int32_t* kprefix;    // [bh, ck + 1]
+    const int32_t* counts;
+    const int32_t* items;
+    uint16_t* out;
+    int cap, oi_rows, kq, kk, bhn, band, sq, sk, cq, ck, shift;
+    float levels, scale_log2;
+};
+
+constexpr int kBoTile = 32;  // keys per tile
+
+template <int DT, int D>
+__global__ __launch_bounds__(256, 2) void bo_attention_kernel(BoAttnArgs A) {
+    using T = Tiles<D>;
+    constexpr int S = D / 16;          // bf16 k-steps of S^T
+    constexpr int S8 = D / 32;         // int8 k-steps
+    constexpr int NB = D / 32;         // 32-channel blocks of O^T
+    constexpr int CW = D / 16;         // 16-byte code chunks per key row
+    constexpr int CH = D / 8;          // 16-byte chunks per 16-bit row
+    constexpr int VCH = kBoTile * CH / 256;  // 16-bit row chunks per thread and tile
+    constexpr float kLazyLog2 = 8.0f;
+    static_assert(VCH >= 1 && kBoTile * CW <= 256, "tile staging assumes 256 threads");
+    __shared__ __align__(16) uint16_t kt_lds[2][kBoTile * D];  // codes (D bytes per row) or K rows
+    __shared__ __align__(16) uint16_t vt_lds[2][kBoTile * D];
+    __shared__ __align__(16) float kq_lds[2][4][kBoTile];      // per key: Cq.k^, Sum(k^), b, t
+    __shared__ __align__(16) float gam[4][32][32];             // per wavefront: u.Ck / cs
+    __shared__ float tile_cs[2];                                // the tile's cluster scale cs
+    __shared__ __align__(16) float cq_lds[D];
+    __shared__ int tmp[4];
+    extern __shared__ int dyn[];
+    const int ck = A.ck;
+    int* cl_start = dyn;           // kept, non-empty key clusters of the map row, in order
+    int* cl_size = dyn + ck;
+    int* cl_kc = dyn + 2 * ck;
+
+    const int per_band = A.band * A.cap;
+    const int in_band = blockIdx.x % per_band;
+    const int bh = (blockIdx.x / per_band) * A.band + in_band % A.band;
+    const int slot = in_band / A.band;
+    if (slot >= A.counts[bh]) return;
+    const int32_t* item = A.items + (static_cast<int64_t>(bh) * A.cap + slot) * 3;
+    const int q_start = item[0], qc = item[1], q_rows = item[2];
+    const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave, h = lane / 32;
+    const int64_t head = bh;
+    const bool video_q = qc < A.kq;
+    const uint32_t sq_last = static_cast<uint32_t>(A.sq - 1);
+
+    // Query rows: wavefront w holds rows 32w .. 32w+31 of the item, lane l row l % 32 with
+    // channels 16s + 8h .. +7 (the bf16 operand layout).
+    const int qrow = wave * 32 + lane % 32;
+    const bool qvalid = qrow < q_rows;
+    const bool wave_active = wave * 32 < q_rows;
+    int64_t qsrc = q_start + qrow;
+    if (qvalid && qsrc < A.oi_rows) qsrc = min(static_cast<uint32_t>(A.out_index[head * A.oi_rows + qsrc]), sq_last);
+    u16x8 qf[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+        qf[s] = qvalid ? *reinterpret_cast<const u16x8*>(A.q + (head * A.sq + qsrc) * D + 16 * s + 8 * h)
+                       : u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    f32x8 qcr[S];
+    const float* crow = A.q_cent + (head * A.kq + min(qc, A.kq - 1)) * D;
+#pragma unroll
+    for (int s = 0; s < S; ++s) qcr[s] = video_q ? *reinterpret_cast<const f32x8*>(crow + 16 * s + 8 * h) : f32x8{};
+    if (tid < D) cq_lds[tid] = video_q ? crow[tid] : 0.0f;
+
+    // Kept key clusters of this map row with their clamped row ranges, and the tile count.
+    int nk, ntiles;
+    {
+        const uint8_t* sel = A.selected + (head * A.cq + qc) * ck;
+        const int32_t* gk = A.kprefix + head * (ck + 1);
+        const int per = static_cast<int>(ceil_div(ck, 256));
+        const int c0 = tid * per, c1 = min(ck, c0 + per);
+        int lcount = 0, ltiles = 0;
+        for (int c = c0; c < c1; ++c) {
+            const int a = gk[c], e = gk[c + 1];
+            if (sel[c] && e > a) {
+                ++lcount;
+                ltiles += static_cast<int>(ceil_div(e - a, kBoTile));
+            }
+        }
+        int idx = block_scan<4>(lcount, tmp, &nk);
+        block_scan<4>(ltiles, tmp, &ntiles);
+        for (int c = c0; c < c1; ++c) {
+            const int a = gk[c], e = gk[c + 1];
+            if (sel[c] && e > a) {
+                cl_start[idx] = a;
+                cl_size[idx] = e - a;
+                cl_kc[idx] = c;
+                ++idx;
+            }
+        }
+    }
+
+    // Video rows: Base-Offset quantization at load (base_offset.hpp, the quantizer's own
+    // arithmetic): codes u, row low a and scale s, and the fake-quantized row in qf for the
+    // bf16 tiles. The int8 operand of k-step s8 holds channels 32 s8 + 16h .. +15: channels
+    // 16 sg + 8e .. +7 (sg = 2 s8 + h) come from this lane for e = h and from lane l ^ 32 for
+    // e = 1 - h.
+    u32x4 u8op[S8];
+    float qa = 0.0f, qs = 0.0f, qu = 0.0f, cq_sum = 0.0f;
+    if (video_q) {
+        float lo = INFINITY, hi = -INFINITY;
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float r = half_to_f32<DT>(qf[s][i]) - qcr[s][i];
+                lo = fminf(lo, r);
+                hi = fmaxf(hi, r);
+            }
+        lo = fminf(lo, __shfl_xor(lo, 32, kWave));
+        hi = fmaxf(hi, __shfl_xor(hi, 32, kWave));
+        const BaseOffsetRow bo = base_offset_row(lo, hi, A.levels);
+        u32x2 ub[S];
+        int usum = 0;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            ub[s] = u32x2{0u, 0u};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float c = qcr[s][i];
+                uint32_t code;
+                const float xh = base_offset_value(half_to_f32<DT>(qf[s][i]) - c, c, bo, code);
+                qf[s][i] = f32_to_half<DT>(xh);
+                usum += static_cast<int>(code);
+                ub[s][i / 4] |= ((code - static_cast<uint32_t>(A.shift)) & 0xffu) << (8 * (i % 4));
+                cq_sum += c;
+            }
+        }
+#pragma unroll
+        for (int s8 = 0; s8 < S8; ++s8) {
+            const u32x2 mine = ub[2 * s8 + h];
+            const u32x2 send = ub[2 * s8 + 1 - h];
+            const u32x2 recv{static_cast<uint32_t>(__shfl_xor(static_cast<int>(send[0]), 32, kWave)),
+                             static_cast<uint32_t>(__shfl_xor(static_cast<int>(send[1]), 32, kWave))};
+            u8op[s8] = h == 0 ? u32x4{mine[0], mine[1], recv[0], recv[1]} : u32x4{recv[0], recv[1], mine[0], mine[1]};
+        }
+        qu = static_cast<float>(usum + __shfl_xor(usum, 32, kWave) - A.shift * D);
+        cq_sum += __shfl_xor(cq_sum, 32, kWave);
+        qs = bo.scale;
+        qa = bo.low + static_cast<float>(A.shift) * bo.scale;
+    } else {
+#pragma unroll
+        for (int s8 = 0; s8 < S8; ++s8) u8op[s8] = u32x4{0u, 0u, 0u, 0u};
+    }
+    __syncthreads();  // the cluster list and cq_lds
+
+    // Tile t covers keys [32 blk, 32 blk + 32) of kept cluster ci. Staging: every thread loads
+    // its share of the next tile into registers during the current one and writes it to LDS
+    // at the end. 16-bit rows: chunk j of thread t is (row, chunk) of (t + 256 j); code rows:
+    // thread t < 32 CW holds row t / CW, chunk t % CW (the CW threads of a row are adjacent).
+    const int crow_t = tid / CW, cchunk = tid % CW;
+    const bool code_thread = tid < kBoTile * CW;
+    u32x4 kreg[VCH], vreg[VCH];  // K rows, or the codes chunk in kreg[0]
+    float klow = 0.0f, kscale = 0.0f, ksum_c = 0.0f, qk = 0.0f, kcs = 0.0f;
+    const uint32_t xmask = A.shift ? 0x80808080u : 0u;
+    auto cluster_of = [&](int ci_, int blk_, int& start, int& nvalid, int& kc, bool& int8) {
+        start = cl_start[ci_] + kBoTile * blk_;
+        nvalid = min(kBoTile, cl_size[ci_] - kBoTile * blk_);
+        kc = cl_kc[ci_];
+        int8 = video_q && kc < A.kk;
+    };
+    auto issue = [&](int ci_, int blk_) __attribute__((always_inline)) {
+        int start, nvalid, kc;
+        bool int8;
+        cluster_of(ci_, blk_, start, nvalid, kc, int8);
+#pragma unroll
+        for (int j = 0; j < VCH; ++j) {
+            const int idx = tid + 256 * j, r = idx / CH, c = idx % CH;
+            const int64_t p = start + (r < nvalid ? r : 0);  // rows past the cluster repeat its first
+            vreg[j] = *reinterpret_cast<const u32x4*>(A.v + (head * A.sk + p) * D + c * 8);
+            if (!int8) kreg[j] = *reinterpret_cast<const u32x4*>(A.k + (head * A.sk + p) * D + c * 8);
+        }
+        if (int8 && code_thread) {
+            const int64_t p = min(start + (crow_t < nvalid ? crow_t : 0), A.oi_rows - 1);
+            kreg[0] = *reinterpret_cast<const u32x4*>(A.k_codes + (head * A.oi_rows + p) * D + cchunk * 16);
+            if (cchunk == 0) {
+                klow = A.k_low[head * A.oi_rows + p];
+                kscale = A.k_scale[head * A.oi_rows + p];
+                ksum_c = A.kc_sum[head * A.kk + kc];
+                qk = A.qk_dot[(head * A.kk + kc) * A.kq + qc];
+                kcs = A.kc_scale[head * A.kk + kc];
+            }
+        }
+    };
+    auto stage = [&](int buf, int ci_, int blk_) __attribute__((always_inline)) {
+        int start, nvalid, kc;
+        bool int8;
+        cluster_of(ci_, blk_, start, nvalid, kc, int8);
+#pragma unroll
+        for (int j = 0; j < VCH; ++j) {
+            const int idx = tid + 256 * j, r = idx / CH, c = idx % CH;
+            *reinterpret_cast<u32x4*>(&vt_lds[buf][r * D + (c ^ T::swz_v(r)) * 8]) = vreg[j];
+            if (!int8) *reinterpret_cast<u32x4*>(&kt_lds[buf][r * D + (c ^ T::swz_k(r)) * 8]) = kreg[j];
+        }
+        if (int8 && code_thread) {
+            const u32x4 w = kreg[0] ^ u32x4{xmask, xmask, xmask, xmask};
+            uint8_t* kb = reinterpret_cast<uint8_t*>(kt_lds[buf]);
+            *reinterpret_cast<u32x4*>(kb + crow_t * D + ((cchunk ^ (crow_t % CW)) * 16)) = w;
+            // Sum(w) and Cq.w over this chunk's 16 channels, then over the row's CW chunks.
+            int sw = 0;
+            float cw = 0.0f;
+#pragma unroll
+            for (int d4 = 0; d4 < 4; ++d4) {
+                const f32x4 cq4 = *reinterpret_cast<const f32x4*>(&cq_lds[cchunk * 16 + 4 * d4]);
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const int val = static_cast<int8_t>((w[d4] >> (8 * b)) & 0xffu);
+                    sw += val;
+                    cw = __builtin_fmaf(static_cast<float>(val), cq4[b], cw);
+                }
+            }
+#pragma unroll
+            for (int m = 1; m < CW; m <<= 1) {
+                sw += __shfl_xor(sw, m, kWave);
+                cw += __shfl_xor(cw, m, kWave);
+            }
+            if (cchunk == 0) {
+                const bool valid = crow_t < nvalid;
+                const float t = kscale;
+                const float b = klow + static_cast<float>(A.shift) * kscale;
+                kq_lds[buf][0][crow_t] = valid ? qk + b * cq_sum + t * cw : 0.0f;
+                kq_lds[buf][1][crow_t] = valid ? ksum_c + static_cast<float>(D) * b + t * static_cast<float>(sw) : 0.0f;
+                kq_lds[buf][2][crow_t] = valid ? b : 0.0f;
+                kq_lds[buf][3][crow_t] = valid ? t : 0.0f;
+                if (crow_t == 0) tile_cs[buf] = kcs;
+            }
+        }
+    };
+
+    f32x16 oacc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) oacc[nb] = f32x16{};
+    float m_run = -INFINITY, l_run = 0.0f, neg_m = 0.0f;
+    const float scale_log2 = A.scale_log2;
+    const float lazy = kLazyLog2 / scale_log2;
+    const int gsub = (lane / 16) % 2, src = lane % 16;
+
+    // u.Ck / cs for the wavefront's rows and kept clusters 32 g .. 32 g + 31 (text clusters and
+    // slots past the list give 0, never read): A = the clusters' int8 planes, B = u. One plane
+    // at a time keeps the operands' registers few.
+    auto gamma_block = [&](int g) __attribute__((always_inline)) {
+        const int li = 32 * g + lane % 32;
+        const bool ok = li < nk && cl_kc[min(li, nk - 1)] < A.kk;
+        const int kcm = ok ? cl_kc[li] : 0;
+        const int8_t* pl = A.kc_planes + (head * A.kk + kcm) * 3 * D;
+        f32x16 comb{};
+#pragma unroll 1
+        for (int pn = 0; pn < 3; ++pn) {
+            u32x4 pa[S8];
+#pragma unroll
+            for (int s8 = 0; s8 < S8; ++s8)
+                pa[s8] = ok ? *reinterpret_cast<const u32x4*>(pl + pn * D + 32 * s8 + 16 * h) : u32x4{0u, 0u, 0u, 0u};
+            i32x16 acc{};
+#pragma unroll
+            for (int s8 = 0; s8 < S8; ++s8)
+                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, pa[s8]),
+                                                            __builtin_bit_cast(i32x4, u8op[s8]), acc, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float wt = pn == 0 ? 1.0f : (pn == 1 ? 1.0f / 128.0f : 1.0f / 16384.0f);
+                comb[i] = __builtin_fmaf(static_cast<float>(acc[i]), wt, comb[i]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) gam[wave][8 * (i / 4) + 4 * h + (i % 4)][lane % 32] = comb[i];
+    };
+
+    int ci = 0, blk = 0, gblk = -1;
+    if (ntiles > 0) {
+        issue(0, 0);
+        stage(0, 0, 0);
+    }
+    __syncthreads();
+    for (int t = 0; t < ntiles; ++t) {
+        const int buf = t & 1;
+        int start, nvalid, kc;
+        bool int8;
+        cluster_of(ci, blk, start, nvalid, kc, int8);
+        if (int8 && wave_active && ci / 32 != gblk) {
+            gblk = ci / 32;
+            gamma_block(gblk);
+        }
+        int nci = ci, nblk = blk + 1;
+        if (kBoTile * nblk >= cl_size[ci]) {
+            ++nci;
+            nblk = 0;
+        }
+        const bool more = t + 1 < ntiles;
+        if (more) issue(nci, nblk);
+        if (wave_active) {
+            const int row = lane % 32;
+            f32x16 sacc;
+            if (int8) {
+                const uint8_t* kb = reinterpret_cast<const uint8_t*>(kt_lds[buf]);
+                i32x16 acc{};
+#pragma unroll
+                for (int s8 = 0; s8 < S8; ++s8) {
+                    const u32x4 af = *reinterpret_cast<const u32x4*>(kb + row * D + (((2 * s8 + h) ^ (row % CW)) * 16));
+                    acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, af),
+                                                                __builtin_bit_cast(i32x4, u8op[s8]), acc, 0, 0, 0);
+                }
+                const float gm = gam[wave][ci % 32][row] * tile_cs[buf];
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int kb0 = 8 * g + 4 * h;
+                    const f32x4 bq = *reinterpret_cast<const f32x4*>(&kq_lds[buf][0][kb0]);
+                    const f32x4 sk4 = *reinterpret_cast<const f32x4*>(&kq_lds[buf][1][kb0]);
+                    const f32x4 bk = *reinterpret_cast<const f32x4*>(&kq_lds[buf][2][kb0]);
+                    const f32x4 tk = *reinterpret_cast<const f32x4*>(&kq_lds[buf][3][kb0]);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float x = __builtin_fmaf(tk[i], static_cast<float>(acc[4 * g + i]),
+                                                       __builtin_fmaf(bk[i], qu, gm));
+                        sacc[4 * g + i] = __builtin_fmaf(qs, x, __builtin_fmaf(qa, sk4[i], bq[i]));
+                    }
+                    asm volatile("" ::: "memory");  // keeps each group's per-key reads next to their use
+                }
+            } else {
+                sacc = f32x16{};
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    const int pc = (2 * s + h) ^ T::swz_k(row);
+                    const u16x8 kf = *reinterpret_cast<const u16x8*>(&kt_lds[buf][row * D + pc * 8]);
+                    sacc = Mfma<DT>::run(kf, qf[s], sacc);
+                }
+            }
+            auto read_vt = [&](int kk, int nb) __attribute__((always_inline)) {
+                s16x4 part[2];
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    const int vrow = 16 * kk + 8 * tt + 4 * h + src / 4;
+                    const int d = 32 * nb + 16 * gsub + 4 * (src % 4);
+                    const int pc = (d / 8) ^ T::swz_v(vrow);
+                    const uint16_t* a = &vt_lds[buf][vrow * D + pc * 8 + (d % 8)];
+                    part[tt] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(a));
+                }
+                return __builtin_bit_cast(
+                    u16x8, u32x4{__builtin_bit_cast(u32x2, part[0])[0], __builtin_bit_cast(u32x2, part[0])[1],
+                                 __builtin_bit_cast(u32x2, part[1])[0], __builtin_bit_cast(u32x2, part[1])[1]});
+            };
+            if (nvalid < kBoTile) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    if (8 * (i / 4) + 4 * h + (i % 4) >= nvalid) sacc[i] = -INFINITY;
+            }
+            float tmax = sacc[0];
+#pragma unroll
+            for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, sacc[i]);
+            if (__any(tmax > m_run + lazy)) {
+                tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+                const float m_new = fmaxf(m_run, tmax);
+                const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
+                m_run = m_new;
+                neg_m = -m_new * scale_log2;
+                l_run *= alpha;
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) oacc[nb][i] *= alpha;
+            }
+            uint32_t pp[8];
+#pragma unroll
+            for (int i = 0; i < 16; i += 2) {
+                const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[i], scale_log2, neg_m));
+                const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[i + 1], scale_log2, neg_m));
+                pp[i / 2] = Mfma<DT>::pack2(p0, p1);
+                l_run = Mfma<DT>::sum2(pp[i / 2], l_run);
+            }
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                const u16x8 pf = __builtin_bit_cast(u16x8, u32x4{pp[4 * kk], pp[4 * kk + 1], pp[4 * kk + 2],
+                                                                pp[4 * kk + 3]});
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) {
+                    oacc[nb] = Mfma<DT>::run(read_vt(kk, nb), pf, oacc[nb]);
+                }
+            }
+        }
+        if (more) stage(buf ^ 1, nci, nblk);
+        __syncthreads();
+        ci = nci;
+        blk = nblk;
+    }
+    if (!qvalid) return;
+    const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    int64_t orow = q_start + qrow;
+    if (orow < A.oi_rows) orow = min(static_cast<uint32_t>(A.out_index[head * A.oi_rows + orow]), sq_last);
+    uint16_t* o = A.out + (head * A.sq + orow) * D;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d0 = 32 * nb + 8 * g + 4 * h;
+            const uint32_t w0 = Mfma<DT>::pack2(oacc[nb][4 * g + 0] * inv, oacc[nb][4 * g + 1] * inv);
+            const uint32_t w1 = Mfma<DT>::pack2(oacc[nb][4 * g + 2] * inv, oacc[nb][4 * g + 3] * inv);
+            *reinterpret_cast<u32x2*>(o + d0) = u32x2{w0, w1};
+        }
+}
+
 size_t build_lds_bytes(int cq, int ck) {
     const int cap = kSortCap;
     return sizeof(int) * ((static_cast<size_t>(ck) + 2 * cq + 2) & ~static_cast<size_t>(1)) + sizeof(uint64_t) * cap;
@@ -914,6 +1351,79 @@ PECO_API int peco_sparse_attention_work(const void* q, const void* k, const void
                                    out_index_rows, k_index, q_centroids, q_centroids ? q_clusters : 0,
                                    q_centroids ? bits : 0, bh, sq, sk, d, cq, ck, dtype,
                                    static_cast<hipStream_t>(stream));
+}
+
+// Base-Offset integer-score attention (an extension with no counterpart in the reference; see
+// bo_attention_kernel). Map-driven like peco_sparse_attention_ex (selected, q_sizes, k_sizes
+// as there, extended with the text partition), with Q in original token order (video row
+// j < oi_rows of the cluster order read from row out_index[j], which also places the output)
+// and K, V, the key codes, lows and scales in cluster order, as peco_kmeans_fit_pack writes
+// them. q_centroids [bh, kq, d] and the key centroid planes (kc_planes int8 [bh, kk, 3, d],
+// kc_scale, kc_sum fp32 [bh, kk], qk_dot fp32 [bh, kk, kq] = Ck.Cq) describe the first kq
+// query and kk key clusters of the map (the video ones); bits is the codes' width (4 or 8).
+PECO_API int peco_base_offset_attention(const void* q, const int32_t* out_index, const float* q_centroids, int kq,
+                                        const void* k, const void* v, const uint8_t* k_codes, const float* k_low,
+                                        const float* k_scale, const int8_t* kc_planes, const float* kc_scale,
+                                        const float* kc_sum, const float* qk_dot, int kk, int bits,
+                                        const uint8_t* selected, const int* q_sizes, const int* k_sizes,
+                                        void* output, int* workspace, size_t workspace_ints, int bh, int sq, int sk,
+                                        int oi_rows, int d, int cq, int ck, int dtype, void* stream) {
+    if (!q || !out_index || !q_centroids || !k || !v || !k_codes || !k_low || !k_scale || !kc_planes || !kc_scale ||
+        !kc_sum || !qk_dot || !selected || !q_sizes || !k_sizes || !output || !workspace || bh < 1 || bh > 65535 ||
+        sq < 1 || sk < 1 || cq < 1 || ck < 1 || kq < 1 || kq > cq || kk < 1 || kk > ck || oi_rows < 1 ||
+        oi_rows > sq || oi_rows > sk || (d != 64 && d != 128) || (dtype != kF16 && dtype != kBF16) ||
+        (bits != 4 && bits != 8))
+        return kInvalidValue;
+    if (workspace_ints < peco_sparse_attention_workspace_size(bh, sq, sk, cq, ck)) return kWorkspaceTooSmall;
+    const size_t lds_build = build_lds_bytes(cq, ck);
+    const size_t lds_list = sizeof(int) * 3 * static_cast<size_t>(ck);
+    if (lds_build > 60 * 1024 || lds_list > 24 * 1024) return kUnsupportedShape;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(build_work_kernel<false>, dim3(bh), dim3(256), lds_build, s, selected, q_sizes, k_sizes, nullptr,
+                       workspace, bh, sq, sk, cq, ck);
+    const WorkLayout W = work_layout(workspace, bh, sq, cq, ck);
+    BoAttnArgs a;
+    a.q = static_cast<const uint16_t*>(q);
+    a.out_index = out_index;
+    a.q_cent = q_centroids;
+    a.k = static_cast<const uint16_t*>(k);
+    a.v = static_cast<const uint16_t*>(v);
+    a.k_codes = k_codes;
+    a.k_low = k_low;
+    a.k_scale = k_scale;
+    a.kc_planes = kc_planes;
+    a.kc_scale = kc_scale;
+    a.kc_sum = kc_sum;
+    a.qk_dot = qk_dot;
+    a.selected = selected;
+    a.kprefix = W.kprefix;
+    a.counts = W.counts;
+    a.items = W.items;
+    a.out = static_cast<uint16_t*>(output);
+    a.cap = W.cap;
+    a.oi_rows = oi_rows;
+    a.kq = kq;
+    a.kk = kk;
+    a.bhn = bh;
+    a.band = attention_head_band(bh, sk, d);
+    a.sq = sq;
+    a.sk = sk;
+    a.cq = cq;
+    a.ck = ck;
+    a.shift = bits == 8 ? 128 : 0;
+    a.levels = static_cast<float>((1 << bits) - 1);
+    a.scale_log2 = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(d)));
+    const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(W.cap) * bh));
+#define PECO_BO(DT_, D_) hipLaunchKernelGGL((bo_attention_kernel<DT_, D_>), grid, dim3(256), lds_list, s, a)
+    if (dtype == kBF16) {
+        if (d == 128) PECO_BO(kBF16, 128);
+        else PECO_BO(kBF16, 64);
+    } else {
+        if (d == 128) PECO_BO(kF16, 128);
+        else PECO_BO(kF16, 64);
+    }
+#undef PECO_BO
+    return hipGetLastError();
 }
 
 // Reference ABI (peco/kernels/sparse_attention.cu:210): workspace holds

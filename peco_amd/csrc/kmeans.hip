@@ -65,10 +65,14 @@ struct KmProblem {
     // receive x's rows in cluster order, Base-Offset fake-quantized (hat_bits) against the
     // final centres, and rows [tokens, length) x's own rows past `tokens` (text, in the same
     // batch stride); with_in/with_out (nullable, [batch, length, D]) are gathered alike
-    // without quantization.
+    // without quantization. codes/low/scale (nullable together, [batch, tokens, D] uint8 and
+    // [batch, tokens] fp32) receive the packed rows' Base-Offset payload in the same order.
     void* hat;
     const void* with_in;
     void* with_out;
+    uint8_t* codes;
+    float* low;
+    float* scale;
     int hat_bits;
     int length;
 };
@@ -841,6 +845,17 @@ __device__ __forceinline__ void pack_members(const KmProblem& P, int b, int begi
                     const int64_t dst = (static_cast<int64_t>(b) * P.length + m0 + r) * D + sub * 8;
                     Row8<DT>::store(P.hat, dst, out);
                     if (with) wv[u].store(P.with_out, dst);
+                    if (P.codes) {
+                        const int64_t row = static_cast<int64_t>(b) * P.tokens + m0 + r;
+                        u32x2 packed;
+                        packed[0] = q[0] | (q[1] << 8) | (q[2] << 16) | (static_cast<uint32_t>(q[3]) << 24);
+                        packed[1] = q[4] | (q[5] << 8) | (q[6] << 16) | (static_cast<uint32_t>(q[7]) << 24);
+                        *reinterpret_cast<u32x2*>(P.codes + row * D + sub * 8) = packed;
+                        if (sub == 0) {
+                            P.low[row] = lo;
+                            P.scale[row] = sc;
+                        }
+                    }
                 }
             }
         }
@@ -1130,6 +1145,9 @@ struct KmFitDesc {
     void* hat = nullptr;             // packing by the last update (see KmProblem)
     const void* with_in = nullptr;
     void* with_out = nullptr;
+    uint8_t* codes = nullptr;
+    float* low = nullptr;
+    float* scale = nullptr;
     int hat_bits = 0;
     int length = 0;
 };
@@ -1200,6 +1218,9 @@ hipError_t km_fit(const KmFitDesc* descs, int num, int dims, int dtype, int iter
         P.hat = d.hat;
         P.with_in = d.with_in;
         P.with_out = d.with_out;
+        P.codes = d.codes;
+        P.low = d.low;
+        P.scale = d.scale;
         P.hat_bits = d.hat_bits;
         P.length = d.length;
         if (d.hat) {
@@ -1315,16 +1336,21 @@ PECO_API int peco_kmeans_fit(int num_problems, const void* const* x, const int64
 // [0, tokens) = x's rows in the final cluster order, Base-Offset fake-quantized with bits[i]
 // against the final centres; rows [tokens, length) = x's rows there, so x_batch_stride[i]
 // must cover length rows), and with_in[i] -> with_out[i] ([batch, length, dims], nullable)
-// gathered in the same order with its text rows copied.
+// gathered in the same order with its text rows copied. codes[i], low[i] and scale[i]
+// (nullable together; uint8 [batch, tokens, dims], fp32 [batch, tokens]) receive the codes,
+// row lows and row scales of hat[i]'s rows [0, tokens), as peco_base_offset_encode writes
+// them (peco/quantization.py:97-128), in the same cluster order.
 PECO_API int peco_kmeans_fit_pack(int num_problems, const void* const* x, const int64_t* x_batch_stride,
                                   const float* const* centers_in, float* const* centers_out, int32_t* const* labels,
                                   int32_t* const* counts, int32_t* const* sorted_indices, int32_t* const* offsets,
                                   const int* batch, const int* tokens, const int* clusters, int dims, int dtype,
                                   int iterations, void* const* hat, const int* bits, const void* const* with_in,
-                                  void* const* with_out, int length, void* workspace, size_t workspace_bytes,
+                                  void* const* with_out, uint8_t* const* codes, float* const* low,
+                                  float* const* scale, int length, void* workspace, size_t workspace_bytes,
                                   void* stream) {
     if (num_problems < 1 || num_problems > kMaxKm || iterations < 1 || (dims != 64 && dims != 128) ||
-        (dtype != kBF16 && dtype != kF16 && dtype != kF32) || !workspace || !hat || !bits || !with_in || !with_out)
+        (dtype != kBF16 && dtype != kF16 && dtype != kF32) || !workspace || !hat || !bits || !with_in || !with_out ||
+        !codes || !low || !scale)
         return kInvalidValue;
     KmFitDesc d[kMaxKm];
     size_t need = 0;
@@ -1342,7 +1368,11 @@ PECO_API int peco_kmeans_fit_pack(int num_problems, const void* const* x, const 
             d[i].with_in = with_in[i];
             d[i].with_out = with_out[i];
             d[i].length = length;
-        } else if (with_in[i] || with_out[i]) {
+            if (!codes[i] != !low[i] || !codes[i] != !scale[i]) return kInvalidValue;
+            d[i].codes = codes[i];
+            d[i].low = low[i];
+            d[i].scale = scale[i];
+        } else if (with_in[i] || with_out[i] || codes[i] || low[i] || scale[i]) {
             return kInvalidValue;
         }
         need += km_workspace_bytes(batch[i], tokens[i], clusters[i], dims);

@@ -20,7 +20,7 @@ import torch.nn.functional as F
 from torch.nn.attention import SDPBackend, sdpa_kernel
 
 from . import clustering_cuda
-from .attention_cuda import sparse_attention, sparse_attention_work
+from .attention_cuda import base_offset_attention, sparse_attention, sparse_attention_work
 from .quantization import _validate_bits
 
 
@@ -138,6 +138,10 @@ class PecoAttention:
         self.k_centroids = None
         self._last_fit = None
         self._last_pack = None
+        # Opt-in extension, not part of the reference's configuration: with Base-Offset on,
+        # score video rows against video keys from the codes on the integer MFMA
+        # (attention_cuda.base_offset_attention) instead of the fake-quantized rows.
+        self.integer_scores = False
 
     def reset(self):
         self.q_centroids = self.k_centroids = None
@@ -151,7 +155,8 @@ class PecoAttention:
         with sizes [B,H,K]. Both fits run in the same launches. With ``pack_keys = (bits,
         key_full, value_full)`` ([B,H,S,D], key the tensor whose video part is ``key``) the
         last update also writes K Base-Offset fake-quantized and V, both in the final key
-        cluster order with the text rows after them, into ``self._last_pack``.
+        cluster order with the text rows after them, into ``self._last_pack``; a fourth entry
+        ``True`` in ``pack_keys`` adds the keys' codes, lows and scales in that order.
         """
         batch, heads, length, dim = query.shape
         initializing = self.q_centroids is None
@@ -175,16 +180,19 @@ class PecoAttention:
         else:
             # The key rows are fitted in place in the full [B*H, S, D] tensor, whose rows past
             # the video part (the text) the packing copies.
-            bits, key_full, value_full = pack_keys
+            bits, key_full, value_full = pack_keys[:3]
+            with_codes = len(pack_keys) > 3 and pack_keys[3]
             full = key_full.shape[2]
             if key_full.dtype != k_flat.dtype or not key_full.is_contiguous() or not value_full.is_contiguous():
                 raise ValueError("the packed key and value must be contiguous [B,H,S,D] tensors like key")
             k_rows = key_full.reshape(batch * heads, full, dim)[:, :length]
             value_flat = value_full.reshape(batch * heads, full, dim)
             problems = [clustering_cuda.KMeansProblem(q_flat, q_init), clustering_cuda.KMeansProblem(k_rows, k_init)]
-            outs, packed = clustering_cuda.kmeans_fit(problems, iterations, pack=[None, (bits, full, value_flat)])
-            k_hat, v_perm = packed[1]
-            self._last_pack = (k_hat.view(batch, heads, full, dim), v_perm.view(batch, heads, full, dim))
+            outs, packed = clustering_cuda.kmeans_fit(problems, iterations,
+                                                      pack=[None, (bits, full, value_flat, with_codes)])
+            k_hat, v_perm = packed[1][:2]
+            self._last_pack = (k_hat.view(batch, heads, full, dim), v_perm.view(batch, heads, full, dim),
+                               *packed[1][2:])
         (q_labels, q_cent, q_sizes, q_idx, _), (k_labels, k_cent, k_sizes, k_idx, _) = outs
         self.q_centroids, self.k_centroids = q_cent, k_cent
         self._last_fit = (q_idx, k_idx)
@@ -225,9 +233,21 @@ class PecoAttention:
         query, key, value = query.contiguous(), key.contiguous(), value.contiguous()
         # With Base-Offset on, the last k-means update also writes K fake-quantized and V in
         # key-cluster order (stages 2-3 of K/V fused into the fit).
+        integer = bool(bits) and self.integer_scores
         q_labels, k_labels, q_sizes, k_sizes = self._update_cluster_state(
-            query[:, :, :video_length], key[:, :, :video_length], pack_keys=(bits, key, value) if bits else None)
+            query[:, :, :video_length], key[:, :, :video_length],
+            pack_keys=(bits, key, value, integer) if bits else None)
         q_idx, k_idx = self._last_fit
+        if integer:
+            # Extension: video x video scores from the Base-Offset codes (see __init__).
+            dynamic_map, ext_q, ext_k = clustering_cuda.select_connections(
+                self.q_centroids.reshape(batch, heads, -1, dim), self.k_centroids.reshape(batch, heads, -1, dim),
+                q_sizes, k_sizes, self.config.top_p,
+                math.ceil(self.config.min_kc_ratio * self.config.num_k_centroids), (valid_text, text_length))
+            k_perm, v_perm, k_codes, k_low, k_scale = self._last_pack
+            return base_offset_attention(query, k_perm, v_perm, dynamic_map, ext_q, ext_k, out_index=q_idx,
+                                         q_centroids=self.q_centroids, k_centroids=self.k_centroids,
+                                         k_codes=k_codes, k_low=k_low, k_scale=k_scale, bits=bits)
         # Cluster connectivity from the floating-point centres, extended with the text
         # partition (select_cluster_connections + extend_text_partition), in one launch that
         # also writes each query cluster's kept key segments and the attention's work items.
@@ -244,7 +264,7 @@ class PecoAttention:
         # K (fake-quantized) and V come packed from the fit; Q is read in its original order
         # through the permutation and fake-quantized as the attention loads it. Video rows
         # return to their original positions; text rows keep theirs.
-        k_perm, v_perm = self._last_pack
+        k_perm, v_perm = self._last_pack[:2]
         return sparse_attention_work(query, k_perm, v_perm, work, out_index=q_idx, out_index_rows=video_length,
                                      q_centroids=self.q_centroids, bits=bits)
 

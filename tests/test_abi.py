@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_library_loads_and_reports_status_strings_without_a_gpu():
     lib = _native.library()
-    assert lib.peco_abi_version() == 3
+    assert lib.peco_abi_version() == 4
     assert b"workspace" in lib.peco_cluster_error_message(20001)
     assert lib.peco_attention_error_string(0)
     # Size queries are host-only arithmetic.
@@ -65,6 +65,14 @@ def test_work_list_entries_reject_bad_arguments_and_size_the_buffer():
                                 null, 1 << 20, null) == 1
     assert lib.peco_sparse_attention_work(null, null, null, null, null, 0, null, null, 0, 0, null, 0, 1, 16, 16, 128,
                                           4, 4, 1, null) == 1
+
+
+def test_base_offset_attention_rejects_bad_arguments():
+    lib = _native.library()
+    null = ctypes.c_void_p(0)
+    args = [null, null, null, 4, null, null, null, null, null, null, null, null, null, 8, 4, null, null, null, null,
+            null, 1 << 20, 1, 64, 64, 60, 128, 6, 10, 1, null]
+    assert lib.peco_base_offset_attention(*args) == 1
 
 
 def test_library_leaves_no_own_symbol_undefined():
