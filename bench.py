@@ -418,6 +418,71 @@ def measure(name, steps, warmup, stage_reps, attn_reps=20):
     return out, wl
 
 
+def measure_integer_scores(name, steps, warmup, reps):
+    """The Base-Offset layer with integer scores (PecoAttention.integer_scores, an extension
+    with no counterpart in the reference): ms per layer step, and the integer-score attention
+    launch against the launch over rounded reconstructions on the same selection."""
+    from peco_amd import attention_cuda, clustering_cuda, workloads
+
+    wl = workloads.make_workload(name, device=torch.device("cuda:0"))
+    s = wl.shape
+    n, heads, dim = s.video, s.heads, s.dims
+    layer = make_layer(wl)
+    layer.integer_scores = True
+    q, k, v = wl.query, wl.key, wl.value
+    with torch.no_grad():
+        for _ in range(warmup):
+            run_step(layer, wl, q, k, v, wl.q_init, wl.k_init)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            run_step(layer, wl, q, k, v, wl.q_init, wl.k_init)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        layer.q_centroids, layer.k_centroids = wl.q_init, wl.k_init
+        _, _, qs, ks = layer._update_cluster_state(q[:, :, :n], k[:, :, :n], pack_keys=(s.bits, k, v, True))
+        q_idx, _ = layer._last_fit
+        kp, vp, codes, low, scale = layer._last_pack
+        minimum = math.ceil(wl.min_kc_ratio * s.num_k_centroids)
+        qc4 = layer.q_centroids.reshape(1, heads, -1, dim)
+        kc4 = layer.k_centroids.reshape(1, heads, -1, dim)
+        emap, eqs, eks = clustering_cuda.select_connections(qc4, kc4, qs, ks, wl.top_p, minimum,
+                                                            text=(s.text, s.text))
+        work = clustering_cuda.select_work(qc4, kc4, qs, ks, wl.top_p, minimum, (s.text, s.text), q.shape[2],
+                                           q.shape[2])
+        flops = workloads.attention_flops(emap, eqs, eks, dim)
+
+        def integer():
+            return attention_cuda.base_offset_attention(
+                q, kp, vp, emap, eqs, eks, out_index=q_idx, q_centroids=layer.q_centroids,
+                k_centroids=layer.k_centroids, k_codes=codes, k_low=low, k_scale=scale, bits=s.bits)
+
+        def rounded():
+            return attention_cuda.sparse_attention_work(q, kp, vp, work, out_index=q_idx, out_index_rows=n,
+                                                        q_centroids=layer.q_centroids, bits=s.bits)
+
+        times = {}
+        for label, fn in (("integer", integer), ("rounded", rounded)):
+            for _ in range(2):
+                fn()
+            torch.cuda.synchronize()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            for _ in range(reps):
+                fn()
+            end.record()
+            torch.cuda.synchronize()
+            times[label] = start.elapsed_time(end) / reps
+    return {
+        "ms_per_step": round(ms, 4), "value": round(flops / (ms * 1e-3) / 1e12, 3), "steps": steps,
+        "attention_ms": round(times["integer"], 4),
+        "attention_tflops": round(flops / (times["integer"] * 1e-3) / 1e12, 2),
+        "rounded_attention_ms": round(times["rounded"], 4),
+        "note": "video x video scores from the Base-Offset codes on v_mfma_i32_32x32x32_i8 (extension); "
+                "attention_ms includes the centroid-plane preparation launches",
+    }
+
+
 # The other benchmark configurations, timed in the default run after the headline one:
 # (workload, steps, warmup, stage reps, attention reps); the denoising sequence separately.
 OTHER_WORKLOADS = (("hunyuan_480p_bo4", 20, 3, 5, 20), ("hunyuan_720p", 3, 1, 2, 5))
@@ -454,6 +519,8 @@ def main():
         for name, steps, warmup, stage_reps, attn_reps in OTHER_WORKLOADS:
             others[name], _ = measure(name, steps, warmup, stage_reps, attn_reps)
             torch.cuda.empty_cache()
+        others["hunyuan_480p_bo4_integer_scores"] = measure_integer_scores("hunyuan_480p_bo4", 10, 2, 10)
+        torch.cuda.empty_cache()
         name, steps, warmup = SEQUENCE_WORKLOAD
         seq = run_sequence(name, steps, warmup)
         others[name + "_sequence"] = {k_: v_ for k_, v_ in seq.items() if k_ not in line or k_ in ("value", "steps",
