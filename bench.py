@@ -46,7 +46,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--stage-reps", type=int, default=10)
-    ap.add_argument("--profile-target", choices=("attention", "kmeans", "pack", "copy"), default=None,
+    ap.add_argument("--profile-target", choices=("attention", "kmeans", "pack", "copy", "integer"), default=None,
                     help="replay only the attention launch, the Q+K k-means fit, the pack launch (fake-quant and "
                          "gather; Base-Offset workloads) or a plain device copy of --copy-mib MiB, --reps times "
                          "(for rocprofv3 counter runs)")
@@ -234,6 +234,11 @@ def profile_target(args):
         torch.cuda.synchronize()
         print(f"copy {args.copy_mib} MiB x {args.reps}: reads {args.copy_mib * 1024} KiB and writes "
               f"{args.copy_mib * 1024} KiB per dispatch", flush=True)
+        return
+    if args.profile_target == "integer":
+        # The integer-score attention and the launch over rounded rows on the same selection
+        # (Base-Offset workloads), each args.reps times after two untimed calls.
+        print(json.dumps(measure_integer_scores(args.workload, 1, 1, args.reps)), flush=True)
         return
     from peco_amd import clustering_cuda, workloads
 
