@@ -188,9 +188,11 @@ size_t peco_select_work_size(int bh, int sq, int cq, int ck, int extend);
  * rows, adjacent ones merged, each as {first physical row - stream offset, stream offset}) and
  * its stream length, and, per entry, the attention items in cost order (the entry's last
  * workgroup to finish orders them). map, ext_q and ext_k are optional here. The first bh
- * int32 of work (8-byte aligned) are arrival counters: zero before the first call on a buffer,
- * and every call leaves them zero, so one buffer serves calls ordered on a stream but not
- * overlapping calls. sq and sk are the attention's query and key lengths (video + text). */
+ * int32 of work (8-byte aligned) are arrival counters, and 16 int32 after the items are the
+ * attention's item queue counters: both zero before the first call on a buffer (allocate it
+ * zeroed), and every selection (arrival counters) and attention (queue counters) call leaves
+ * them zero, so one buffer serves calls ordered on a stream but not overlapping calls. sq and
+ * sk are the attention's query and key lengths (video + text). */
 int peco_select_work(const float* qc, const float* kc, const int32_t* q_counts, const int32_t* k_counts, int bh,
                      int cq, int ck, int dims, float p, int minimum, int extend, int valid_text, int text, int sq,
                      int sk, uint8_t* map, int32_t* ext_q, int32_t* ext_k, int32_t* work, size_t work_ints,

@@ -279,12 +279,21 @@ class SelectionWork:
     def _layout(self):
         b, re, ce = self.bh, self.rows, self.cols
         cap = -(-self.sq // 128) + min(re, self.sq)
-        head = 2 * b + b * re + b * cap * 3
+        head = 2 * b + b * re + b * cap * 3 + self.QUEUE_INTS
         head += head & 1
         return b, re, ce, cap, head
 
+    # The attention's item queue counters (one per XCD) and exit counter after the items.
+    QUEUE_INTS = 16
+
     def tickets(self):
         return self.buffer[:self.bh]
+
+    def queues(self):
+        """The attention's item queue counters: zero between calls."""
+        b, re, _, cap, _ = self._layout()
+        start = 2 * b + b * re + b * cap * 3
+        return self.buffer[start:start + self.QUEUE_INTS]
 
     def items(self):
         """(count int32 [bh], items int32 [bh, cap, 3]) as views of the buffer."""

@@ -29,6 +29,8 @@ __host__ __device__ inline int item_capacity(int sq, int cq) {
 //   counts int32 [bh]: items per head;
 //   row_keys int32 [bh, re]: the stream length L of every map row;
 //   items int32 [bh, cap, 3]: q_start, query cluster, rows (<= kQTile), by descending cost;
+//   queues int32 [kQueueInts]: the attention's item queue counters (one per XCD) and its exit
+//         counter; zero before the first call, and every attention call leaves them zero;
 //   segs  int2 [bh, re, ce + 2] (8-byte aligned): per map row {segment count n, L}, then n
 //         segments {first physical row - stream offset, stream offset} of its kept key rows
 //         (adjacent kept clusters merged), then the sentinel {0, INT_MAX}.
@@ -37,13 +39,17 @@ struct SelWork {
     int32_t* counts;
     int32_t* row_keys;
     int32_t* items;
+    int32_t* queues;
     int2* segs;
     int cap;
 };
 
+constexpr int kItemQueues = 8;   // attention item queues, one per XCD
+constexpr int kQueueInts = 16;   // the queues' counters and the exit counter, padded
+
 __host__ __device__ inline size_t sel_work_head_ints(int bh, int sq, int re) {
     const size_t b = static_cast<size_t>(bh);
-    const size_t n = 2 * b + b * re + b * item_capacity(sq, re) * 3;
+    const size_t n = 2 * b + b * re + b * item_capacity(sq, re) * 3 + kQueueInts;
     return (n + 1) & ~static_cast<size_t>(1);
 }
 
@@ -59,6 +65,7 @@ __host__ __device__ inline SelWork sel_work_layout(int32_t* base, int bh, int sq
     w.counts = base + bh;
     w.row_keys = w.counts + bh;
     w.items = w.row_keys + static_cast<size_t>(bh) * re;
+    w.queues = w.items + static_cast<size_t>(bh) * w.cap * 3;
     w.segs = reinterpret_cast<int2*>(base + sel_work_head_ints(bh, sq, re));
     return w;
 }

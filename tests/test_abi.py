@@ -56,8 +56,9 @@ def test_work_list_entries_reject_bad_arguments_and_size_the_buffer():
     lib = _native.library()
     null = ctypes.c_void_p(0)
     # 24 heads, 7006 rows, a 66 x 258 extended map: counters, counts, row lengths, items
-    # (55 + 66 per head, 3 ints each), then 8-byte aligned segment rows of 260 int2.
-    head = 2 * 24 + 24 * 66 + 24 * (55 + 66) * 3
+    # (55 + 66 per head, 3 ints each), 16 queue counters, then 8-byte aligned segment rows of
+    # 260 int2.
+    head = 2 * 24 + 24 * 66 + 24 * (55 + 66) * 3 + 16
     head += head & 1
     assert lib.peco_select_work_size(24, 7006, 64, 256, 1) == head + 24 * 66 * 260 * 2
     assert lib.peco_select_work_size(0, 7006, 64, 256, 1) == 0

@@ -89,6 +89,7 @@ def _check_work(work, emap, eqs, eks, sq, sk):
     lengths = work.row_lengths().cpu().numpy()
     counts, items = (t.cpu().numpy() for t in work.items())
     assert not work.tickets().cpu().any(), "arrival counters must be left at zero"
+    assert not work.queues().cpu().any(), "queue counters must be left at zero"
     for b in range(work.bh):
         koff = _clamped_offsets(ksz[b], sk)
         for r in range(work.rows):
@@ -183,7 +184,13 @@ def test_attention_over_work_equals_map_attention(announce, dtype, d, indexed):
         out = attention_cuda.sparse_attention_work(q, k, v, work, out_index=qidx, out_index_rows=video)
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
+    # A second call on the same work list (its item queues reset by the first) gives the same.
+    again = attention_cuda.sparse_attention_work(q, k, v, work, out_index=qidx, out_index_rows=video,
+                                                 k_index=kidx if indexed else None)
+    torch.cuda.synchronize()
+    assert torch.equal(again, out)
     assert not work.tickets().cpu().any()
+    assert not work.queues().cpu().any(), "the attention leaves its queue counters at zero"
 
 
 def test_work_buffer_serves_consecutive_calls(announce):
@@ -198,3 +205,31 @@ def test_work_buffer_serves_consecutive_calls(announce):
         work = clustering_cuda.select_work(*args, (5, 8), sq, sk)
         torch.cuda.synchronize()
         _check_work(work, emap, eqs, eks, sq, sk)
+
+
+@pytest.mark.parametrize("indexed", [True, False])
+def test_persistent_grid_equals_map_attention(announce, indexed):
+    """A launch with at least 8 item slots per resident workgroup (16 heads x 32896 rows, 130 x
+    514 extended map: 387 slots per head) runs the persistent grid, whose workgroups take items
+    from one queue per XCD; it must equal the map-driven attention (one workgroup per item) bit
+    for bit, twice on one work list (the first call resets the queues for the second)."""
+    h, cq, ck, video, text, valid, d = 16, 128, 512, 32640, 256, 200, 64
+    q, k, v, qs, ks, qidx, kidx, qc, kc = _clustered_inputs(7 + indexed, h, cq, ck, video, text, d, torch.bfloat16)
+    length = video + text
+    announce(f"H={h} N={video} CQ={cq} CK={ck} indexed={indexed}")
+    q, k, v, qidx, kidx = (t.to(DEV) for t in (q, k, v, qidx, kidx))
+    args = (qc.to(DEV), kc.to(DEV), qs.to(DEV), ks.to(DEV), 1e-9, 100)
+    emap, eqs, eks, kept = clustering_cuda.select_connections(*args, text=(valid, text), with_kept=True)
+    work = clustering_cuda.select_work(*args, (valid, text), length, length)
+    kw = dict(out_index=qidx, out_index_rows=video)
+    if indexed:
+        ref = attention_cuda.sparse_attention_indexed(q, k, v, emap, eqs, eks, qidx, kidx, video,
+                                                      validate_sizes=False, kept_keys=kept)
+        kw["k_index"] = kidx
+    else:
+        ref = attention_cuda.sparse_attention(q, k, v, emap, eqs, eks, validate_sizes=False, kept_keys=kept, **kw)
+    for _ in range(2):
+        out = attention_cuda.sparse_attention_work(q, k, v, work, **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+        assert not work.queues().cpu().any()
