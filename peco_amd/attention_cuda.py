@@ -246,7 +246,8 @@ def sparse_attention_work(
 
 def centroid_planes(centroids: torch.Tensor):
     """Key centroids [BH, K, D] fp32 as three int8 planes and a scale per centroid:
-    C = cs * (P0 + P1/128 + P2/16384) to within 2^-22 * max|C| of each centroid, plus Sum(C).
+    C = cs * (P0 + P1/128 + P2/16384) to within 2^-21 * max|C| of each centroid (the last
+    plane's half step, 2^-22, plus the fp32 rounding of C / cs), plus Sum(C).
 
     Returns (planes int8 [BH, K, 3, D], cs fp32 [BH, K], sums fp32 [BH, K]). cs = max|C|/127
     (1 for a zero centroid); each plane is the rounded remainder of the one before, scaled

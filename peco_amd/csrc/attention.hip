@@ -839,7 +839,7 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
 // - u.w, the only term over query row x key, is exact int32 from v_mfma_i32_32x32x32_i8
 //   (half the MFMA issue of the bf16 S^T).
 // - u.Ck (query row x key cluster) also runs on the integer MFMA, against the key centroids
-//   held as three int8 planes, Ck = cs*(P0 + P1/128 + P2/16384) to within 2^-22 |Ck|max,
+//   held as three int8 planes, Ck = cs*(P0 + P1/128 + P2/16384) to within 2^-21 |Ck|max,
 //   for 32 kept clusters at a time, into an LDS table per wavefront.
 // - Cq.w and Sum(w) are reduced per key from its codes while the tile is staged; Cq.Ck and
 //   Sum(Ck) come per tile, Sum(u), a and s per row.
