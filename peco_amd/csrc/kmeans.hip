@@ -31,6 +31,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 #include <vector>
 
 namespace peco {
@@ -51,6 +52,8 @@ struct KmProblem {
     int32_t* tile_hist;     // [batch, sort tiles, K] (cleared by the prep kernel)
     int32_t* tile_hist2;    // nullable second histogram set: alternates with tile_hist per iteration
     float* sums;            // nullable [batch, K, D]: per-cluster sums of the last update
+    float* xsq;             // nullable [batch, tokens]: squared token norms (certification bound),
+                            // written by the first assign of a fit and read by the later ones
     int batch, tokens, clusters;
     int assign_begin;       // first linear assign block of this problem
     int assign_blocks;      // batch * ceil(tokens / kAssignTile)
@@ -99,6 +102,8 @@ struct KmIter {
     float* dst[kMaxKm];        // means written by this iteration
     int32_t* hist[kMaxKm];     // nullable: tile histograms the assign adds its labels to
     float* screen;             // kDump assignments only: screened distances [batch, tokens, K]
+    int sq_mode;               // token norms: 0 computed by the assign, 1 computed and stored to
+                               // P.xsq, 2 read from P.xsq (x is the same in every iteration)
 };
 
 namespace {
@@ -179,7 +184,7 @@ __device__ __forceinline__ XChunk<DT> load_x8(const void* x, int64_t e) {
 }
 
 // fp16/fp32 rows: load and split one chunk (hi, lo) in place; zero for an invalid token.
-template <int DT>
+template <int DT, bool kSq = true>
 __device__ __forceinline__ void load_split_x8(const void* x, int64_t e, bool valid, u16x8& hi, u16x8& lo, float& sq) {
     if (!valid) {
         hi = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
@@ -202,23 +207,27 @@ __device__ __forceinline__ void load_split_x8(const void* x, int64_t e, bool val
         const uint16_t h = f32_to_bf16_bits(f[i]);
         hi[i] = h;
         lo[i] = f32_to_bf16_bits(f[i] - bf16_bits_to_f32(h));
-        sq = fmaf(f[i], f[i], sq);
+        if constexpr (kSq) sq = fmaf(f[i], f[i], sq);
     }
 }
 
-// bf16 rows: hi of a raw chunk (lo is zero), zero for an invalid token; adds its squares to sq.
-template <int DT>
+// bf16 rows: hi is the raw chunk and lo zero. An invalid token's chunk (a copy of the last row,
+// loaded clamped) is used as it is: its screened values are never read. With kSq the squares of
+// a valid token's chunk are added to sq.
+template <int DT, bool kSq = true>
 __device__ __forceinline__ void split_x8(const XChunk<DT>& r, bool valid, u16x8& hi, u16x8& lo, float& sq) {
     static_assert(DT == kBF16, "split_x8 handles bf16 rows");
-    float part = 0.0f;
+    hi = r.u;
+    lo = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    if constexpr (kSq) {
+        float part = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float f = bf16_bits_to_f32(r.u[i]);
-        hi[i] = valid ? r.u[i] : 0;
-        lo[i] = 0;
-        part = fmaf(f, f, part);
+        for (int i = 0; i < 8; ++i) {
+            const float f = bf16_bits_to_f32(r.u[i]);
+            part = fmaf(f, f, part);
+        }
+        sq += valid ? part : 0.0f;
     }
-    sq += valid ? part : 0.0f;
 }
 
 // Assign: one workgroup = kAssignTile tokens of one (problem, batch); wave w owns tokens
@@ -494,8 +503,8 @@ __global__ __launch_bounds__(kAssignThreads, 2) void km_assign_kernel(KmArgs a, 
     const float n0 = norms[min(tid, K - 1)];
     float nmax = tid < K ? n0 : 0.0f;
 
-    // x row loads are issued before any is used (a token past the end reads the last row and
-    // is masked to zero): both 32-token chunks at once for bf16 input, one chunk at a time
+    // x row loads are issued before any is used (a token past the end reads the last row; only
+    // valid tokens' results are used): both 32-token chunks at once for bf16 input, one chunk at a time
     // when x is split (fp16/fp32), whose raw and split chunks would not fit in registers together.
     int tok[2];
     bool valid[2];
@@ -520,20 +529,38 @@ __global__ __launch_bounds__(kAssignThreads, 2) void km_assign_kernel(KmArgs a, 
 
     u16x8 xh[2][S], xl[2][S];
     float sq[2] = {0.0f, 0.0f};
+    // Squared token norms (for the certification bound only): computed from the rows by the
+    // first assign of a fit, which stores them, and read back by the later ones.
+    auto split_all = [&](auto with_sq) {
+        constexpr bool kSq = decltype(with_sq)::value;
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-        if constexpr (kSplitX) {
-            tok[c] = tile * kAssignTile + wave * 64 + 32 * c + (lane % 32);
-            valid[c] = tok[c] < P.tokens;
-            const int64_t xrow =
-                static_cast<int64_t>(b) * P.x_stride + static_cast<int64_t>(min(tok[c], P.tokens - 1)) * D;
+        for (int c = 0; c < 2; ++c) {
+            if constexpr (kSplitX) {
+                tok[c] = tile * kAssignTile + wave * 64 + 32 * c + (lane % 32);
+                valid[c] = tok[c] < P.tokens;
+                const int64_t xrow =
+                    static_cast<int64_t>(b) * P.x_stride + static_cast<int64_t>(min(tok[c], P.tokens - 1)) * D;
 #pragma unroll
-            for (int s = 0; s < S; ++s) load_split_x8<DT>(P.x, xrow + 16 * s + 8 * h, valid[c], xh[c][s], xl[c][s], sq[c]);
-        } else {
+                for (int s = 0; s < S; ++s)
+                    load_split_x8<DT, kSq>(P.x, xrow + 16 * s + 8 * h, valid[c], xh[c][s], xl[c][s], sq[c]);
+            } else {
 #pragma unroll
-            for (int s = 0; s < S; ++s) split_x8<DT>(raw[c][s], valid[c], xh[c][s], xl[c][s], sq[c]);
+                for (int s = 0; s < S; ++s) split_x8<DT, kSq>(raw[c][s], valid[c], xh[c][s], xl[c][s], sq[c]);
+            }
         }
-        sq[c] += __shfl_xor(sq[c], 32, kWave);
+    };
+    if (it.sq_mode == 2) {
+        split_all(std::false_type{});
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+            sq[c] = P.xsq[static_cast<int64_t>(b) * P.tokens + min(tok[c], P.tokens - 1)];
+    } else {
+        split_all(std::true_type{});
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            sq[c] += __shfl_xor(sq[c], 32, kWave);
+            if (it.sq_mode == 1 && valid[c] && h == 0) P.xsq[static_cast<int64_t>(b) * P.tokens + tok[c]] = sq[c];
+        }
     }
     store_centres<D>(regs, chi[0], clo[0], cn[0], tid);
     __syncthreads();
@@ -1161,6 +1188,7 @@ size_t km_workspace_bytes(int batch, int tokens, int clusters, int dims) {
     add(bkd * sizeof(uint16_t));                    // prep hi
     add(bkd * sizeof(uint16_t));                    // prep lo
     add(static_cast<size_t>(batch) * clusters * sizeof(float));  // norms
+    add(static_cast<size_t>(batch) * tokens * sizeof(float));    // token norms
     add(sort_workspace_ints(batch, tokens, clusters) * sizeof(int32_t));
     if (sort_fusable(tokens, clusters)) add(sort_workspace_ints(batch, tokens, clusters) * sizeof(int32_t));
     return bytes;
@@ -1192,6 +1220,7 @@ hipError_t km_fit(const KmFitDesc* descs, int num, int dims, int dtype, int iter
         P.prep_hi = reinterpret_cast<uint16_t*>(take(bkd * sizeof(uint16_t)));
         P.prep_lo = reinterpret_cast<uint16_t*>(take(bkd * sizeof(uint16_t)));
         P.norms = reinterpret_cast<float*>(take(static_cast<size_t>(d.batch) * d.clusters * sizeof(float)));
+        P.xsq = reinterpret_cast<float*>(take(static_cast<size_t>(d.batch) * d.tokens * sizeof(float)));
         P.tile_hist = reinterpret_cast<int32_t*>(take(sort_workspace_ints(d.batch, d.tokens, d.clusters) * sizeof(int32_t)));
         P.tile_hist2 = sort_fusable(d.tokens, d.clusters)
                            ? reinterpret_cast<int32_t*>(take(sort_workspace_ints(d.batch, d.tokens, d.clusters) *
@@ -1276,6 +1305,7 @@ hipError_t km_fit(const KmFitDesc* descs, int num, int dims, int dtype, int iter
         }
         for (int q = 0; q < num; ++q)
             iters[i].hist[q] = (sa.fused && i % 2 == 1) ? a.p[q].tile_hist2 : a.p[q].tile_hist;
+        iters[i].sq_mode = i == 0 ? 1 : 2;
     }
 #define PECO_FIT(DT_, D_) return run_fit<DT_, D_>(a, iters.data(), iterations, sa, stream)
     if (dims == 128) {
