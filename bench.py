@@ -8,7 +8,8 @@ synthetic (Gaussian mixtures) and resident in HBM before timing starts.
 
 value = effective TFLOP/s = 4*D*sum(kept |Q_i||K_j|) / layer time, the reference's metric.
 The roofline object reports the attention kernel (the dominant MFMA kernel): its
-algorithmic FLOPs over its average duration measured with events on the launch stream.
+algorithmic FLOPs over its average duration in the timed steps, measured with events
+recorded on the launch stream around each of its launches.
 cpu_baseline times the oracle's restatement of the reference CPU torch path on a bounded
 sample of heads of the same workload.
 
@@ -378,9 +379,11 @@ def run_sequence(workload, steps, warmup):
     return line
 
 
-def measure(name, steps, warmup, stage_reps, attn_reps=20):
-    """One workload's layer: ms per step, stage times, realised F4 and the attention roofline."""
-    from peco_amd import workloads
+def measure(name, steps, warmup, stage_reps):
+    """One workload's layer: ms per step, stage times, realised F4 and the attention roofline
+    (the attention launch's average duration over the timed steps, from events recorded on its
+    stream around each launch)."""
+    from peco_amd import attention_cuda, workloads
 
     dev = torch.device("cuda:0")
     wl = workloads.make_workload(name, device=dev)
@@ -392,13 +395,17 @@ def measure(name, steps, warmup, stage_reps, attn_reps=20):
         for _ in range(warmup):
             run_step(layer, wl, q, k, v, q_init, k_init)
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            run_step(layer, wl, q, k, v, q_init, k_init)
-        torch.cuda.synchronize()
-        ms = (time.perf_counter() - t0) * 1e3 / steps
+        launches = attention_cuda.launch_events = []
+        try:
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                run_step(layer, wl, q, k, v, q_init, k_init)
+            torch.cuda.synchronize()
+            ms = (time.perf_counter() - t0) * 1e3 / steps
+        finally:
+            attention_cuda.launch_events = None
+        t_attn = sum(a.elapsed_time(b) for a, b in launches) / len(launches)
         stages, flops, attn_args = stage_breakdown(layer, wl, q, k, v, q_init, k_init, stage_reps)
-        t_attn = attention_kernel_time(attn_args, attn_reps)
     value = flops / (ms * 1e-3) / 1e12
     achieved = flops / (t_attn * 1e-3) / 1e12
     out = {
@@ -490,7 +497,7 @@ def measure_integer_scores(name, steps, warmup, reps):
 
 # The other benchmark configurations, timed in the default run after the headline one:
 # (workload, steps, warmup, stage reps, attention reps); the denoising sequence separately.
-OTHER_WORKLOADS = (("hunyuan_480p_bo4", 20, 3, 5, 20), ("hunyuan_720p", 3, 1, 2, 5))
+OTHER_WORKLOADS = (("hunyuan_480p_bo4", 20, 3, 5), ("hunyuan_720p", 3, 1, 2))
 SEQUENCE_WORKLOAD = ("hunyuan_544p_zipf", 2, 1)
 
 
@@ -521,8 +528,8 @@ def main():
     del wl
     if not args.headline_only and args.workload == "hunyuan_480p":
         others = {}
-        for name, steps, warmup, stage_reps, attn_reps in OTHER_WORKLOADS:
-            others[name], _ = measure(name, steps, warmup, stage_reps, attn_reps)
+        for name, steps, warmup, stage_reps in OTHER_WORKLOADS:
+            others[name], _ = measure(name, steps, warmup, stage_reps)
             torch.cuda.empty_cache()
         others["hunyuan_480p_bo4_integer_scores"] = measure_integer_scores("hunyuan_480p_bo4", 10, 2, 10)
         torch.cuda.empty_cache()
