@@ -164,7 +164,9 @@ int peco_sparse_attention_indexed(const void* q, const void* k, const void* v, c
  * counts int32. With extend != 0 the map is [bh,cq+2,ck+2] with the valid-text/padding
  * groups of peco/processor.py:68-84 and ext_q/ext_k receive the extended sizes. kept_keys
  * (nullable) [bh, cq(+2)] receives the number of key rows each map row keeps (the cost of
- * its query rows for the attention work list). */
+ * its query rows for the attention work list). Shapes: ck <= 2048 and dims <= 256 with
+ * 4*(8*dims + 64*(dims+1)) + 8*ck bytes of LDS at most 64 KiB (dims 128 takes any ck);
+ * larger ones return 20002. */
 int peco_select_cluster_connections(const float* qc, const float* kc, const int32_t* q_counts,
                                     const int32_t* k_counts, int bh, int cq, int ck, int dims, float p, int minimum,
                                     int extend, int valid_text, int text, uint8_t* map, int32_t* ext_q,

@@ -406,7 +406,7 @@ def test_sparse_attention_indexed_equals_packed(announce, dtype, dims, sq, sk, r
 # ---------------------------------------------------------------- selection + text partition
 
 @pytest.mark.parametrize("p,ratio", [(1e-9, 0.25), (0.5, 0.0), (0.9, 0.1), (1.0, 0.0), (0.0, 0.0)])
-@pytest.mark.parametrize("dims,ck", [(128, 70), (64, 70), (128, 256), (128, 1000), (64, 2048)])
+@pytest.mark.parametrize("dims,ck", [(128, 70), (64, 70), (128, 256), (128, 1000), (64, 2048), (192, 300)])
 def test_select_connections_matches_oracle(announce, p, ratio, dims, ck):
     g = _gen(int(p * 100) + dims + ck)
     b, h, cq = 1, 3, 20
