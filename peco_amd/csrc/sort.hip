@@ -19,35 +19,6 @@
 namespace peco {
 namespace {
 
-__device__ __forceinline__ int wave_inclusive_scan(int v) {
-    const int lane = lane_id();
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-        const int y = __shfl_up(v, d, kWave);
-        if (lane >= d) v += y;
-    }
-    return v;
-}
-
-// Exclusive scan across a 256-thread block; returns the exclusive prefix and the total.
-__device__ __forceinline__ int block_exclusive_scan256(int v, int* tmp, int* total) {
-    const int lane = lane_id();
-    const int wave = threadIdx.x / kWave;
-    const int inc = wave_inclusive_scan(v);
-    if (lane == kWave - 1) tmp[wave] = inc;
-    __syncthreads();
-    int base = 0, sum = 0;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        const int t = tmp[w];
-        base += w < wave ? t : 0;
-        sum += t;
-    }
-    __syncthreads();
-    *total = sum;
-    return base + inc - v;
-}
-
 __device__ __forceinline__ int find_problem_by_block(const SortArgs& a, int block) {
     int p = 0;
     while (p + 1 < a.num && block >= a.p[p + 1].block_begin) ++p;
@@ -227,7 +198,6 @@ __global__ __launch_bounds__(64) void sort_place_kernel(SortArgs args) {
     const int32_t* lab = P.labels + static_cast<int64_t>(b) * P.tokens;
     int32_t* idx = P.indices + static_cast<int64_t>(b) * P.tokens;
     int32_t* ranks = P.ranks ? P.ranks + static_cast<int64_t>(b) * P.tokens : nullptr;
-    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
     const int begin = tile * kSortTile;
     const int end = min(P.tokens, begin + kSortTile);
     // All labels of the tile are loaded before ranking starts (16 independent loads per lane).
@@ -242,27 +212,8 @@ __global__ __launch_bounds__(64) void sort_place_kernel(SortArgs args) {
 #pragma unroll
     for (int st = 0; st < kSteps; ++st) {
         const int t = begin + st * kWave + lane;
-        const int raw = labs[st];
-        const bool active = t < end && static_cast<unsigned>(raw) < static_cast<unsigned>(K);
-        const int L = active ? raw : 0;
-        uint64_t eq = __ballot(active);
-        for (int bit = 0; bit < bits; ++bit) {
-            const bool on = active && ((L >> bit) & 1);
-            const uint64_t m = __ballot(on);
-            eq &= ((L >> bit) & 1) ? m : ~m;
-        }
-        const int rank = __popcll(eq & below);
-        const int total = __popcll(eq);
-        const bool last = active && ((eq >> lane) == 1ull);
-        // One wavefront: its LDS reads and writes execute in program order, so the read of
-        // base[L] above precedes the update below without a workgroup barrier (whose memory
-        // fence would also wait for the scattered global stores every step).
-        int pos = 0;
-        if (active) pos = base[L] + rank;
-        __builtin_amdgcn_wave_barrier();
-        if (last) base[L] += total;
-        __builtin_amdgcn_wave_barrier();
-        if (active) {
+        const int pos = place_step(labs[st], t < end, K, bits, base);
+        if (pos >= 0) {
             idx[pos] = t;
             if (ranks) ranks[t] = pos;
         }
@@ -363,28 +314,11 @@ __global__ __launch_bounds__(256) void sort_fused_kernel(SortArgs args) {
     const int bits = K > 1 ? 32 - __builtin_clz(static_cast<unsigned>(K - 1)) : 0;
     int32_t* idx = P.indices + static_cast<int64_t>(b) * P.tokens;
     int32_t* ranks = P.ranks ? P.ranks + static_cast<int64_t>(b) * P.tokens : nullptr;
-    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
 #pragma unroll
     for (int st = 0; st < kSteps; ++st) {
         const int t = begin + st * kWave + lane;
-        const int raw = labs[st];
-        const bool active = t < end && static_cast<unsigned>(raw) < static_cast<unsigned>(K);
-        const int L = active ? raw : 0;
-        uint64_t eq = __ballot(active);
-        for (int bit = 0; bit < bits; ++bit) {
-            const bool on = active && ((L >> bit) & 1);
-            const uint64_t m = __ballot(on);
-            eq &= ((L >> bit) & 1) ? m : ~m;
-        }
-        const int rank = __popcll(eq & below);
-        const int cnt = __popcll(eq);
-        const bool last = active && ((eq >> lane) == 1ull);
-        int pos = 0;
-        if (active) pos = base[L] + rank;
-        __builtin_amdgcn_wave_barrier();
-        if (last) base[L] += cnt;
-        __builtin_amdgcn_wave_barrier();
-        if (active) {
+        const int pos = place_step(labs[st], t < end, K, bits, base);
+        if (pos >= 0) {
             idx[pos] = t;
             if (ranks) ranks[t] = pos;
         }

@@ -66,6 +66,65 @@ inline size_t sort_workspace_ints(int batch, int tokens, int clusters) {
     return static_cast<size_t>(batch) * (sort_tiles(tokens) + sort_scan_groups(tokens)) * clusters;
 }
 
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+    const int lane = __lane_id();
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const int y = __shfl_up(v, d, kWave);
+        if (lane >= d) v += y;
+    }
+    return v;
+}
+
+// Exclusive scan across a 256-thread block; returns the exclusive prefix and the total.
+__device__ __forceinline__ int block_exclusive_scan256(int v, int* tmp, int* total) {
+    const int lane = __lane_id();
+    const int wave = threadIdx.x / kWave;
+    const int inc = wave_inclusive_scan(v);
+    if (lane == kWave - 1) tmp[wave] = inc;
+    __syncthreads();
+    int base = 0, sum = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const int t = tmp[w];
+        base += w < wave ? t : 0;
+        sum += t;
+    }
+    __syncthreads();
+    *total = sum;
+    return base + inc - v;
+}
+
+// One step of a stable counting-sort placement by one wavefront: each lane holds one token
+// (label raw, in_tile false past the entry's end; a label outside [0, K) places nothing).
+// Lanes with the same label are found with one ballot per label bit (bits = ceil(log2 K)),
+// the rank among them is a popcount of the lower lanes (token order kept), and base[L], this
+// wavefront's LDS row of next positions, advances by their count. Returns the token's sorted
+// position, or -1. The wavefront's LDS reads and writes execute in program order, so the
+// read of base[L] precedes the update without a workgroup barrier (whose memory fence would
+// also wait for the caller's scattered global stores every step).
+__device__ __forceinline__ int place_step(int raw, bool in_tile, int K, int bits, int* base) {
+    const int lane = __lane_id();
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
+    const bool active = in_tile && static_cast<unsigned>(raw) < static_cast<unsigned>(K);
+    const int L = active ? raw : 0;
+    uint64_t eq = __ballot(active);
+    for (int bit = 0; bit < bits; ++bit) {
+        const bool on = active && ((L >> bit) & 1);
+        const uint64_t m = __ballot(on);
+        eq &= ((L >> bit) & 1) ? m : ~m;
+    }
+    const int rank = __popcll(eq & below);
+    const int count = __popcll(eq);
+    const bool last = active && ((eq >> lane) == 1ull);
+    int pos = -1;
+    if (active) pos = base[L] + rank;
+    __builtin_amdgcn_wave_barrier();
+    if (last) base[L] += count;
+    __builtin_amdgcn_wave_barrier();
+    return pos;
+}
+
 // Fills block_begin/batch_begin/totals for problems[0..num).
 void sort_args_finalize(SortArgs& args);
 
