@@ -293,3 +293,28 @@ def test_layer_544p_zipf_sequence_full_length_matches_oracle(announce):
         worst = max(worst, err.max().item())
         q_init, k_init = torch.from_numpy(fits["q"][1]), torch.from_numpy(fits["k"][1])
     print(f"[544p sequence] worst max error over {shape.steps} calls: {worst:.3e}", flush=True)
+
+
+@pytest.mark.parametrize("bits", [0, 4])
+def test_layer_head_dim_64_matches_oracle(announce, bits):
+    """The layer at head dimension 64 (the other size the attention and fit kernels take),
+    with and without Base-Offset: permutations and centres bit-exact, output within the
+    attention tolerance of the oracle's layer."""
+    base = workloads.SHAPES["hunyuan_480p_bo4" if bits else "hunyuan_480p"]
+    shape = workloads.LayerShape(**{**base.__dict__, "dims": 64, "heads": 2, "video": 3000, "iterations": 6})
+    wl = workloads.make_workload(shape)
+    iters = shape.iterations
+    announce(f"D=64 bits={bits} heads=2 video=3000 iters={iters}")
+    layer, out = _run_layer(wl, iters)
+    ref, _ = _oracle_layer(wl, iters)
+    n = shape.video
+    q_idx, k_idx = layer._last_fit
+    for x, init, idx, cent in ((wl.query, wl.q_init, q_idx, layer.q_centroids),
+                               (wl.key, wl.k_init, k_idx, layer.k_centroids)):
+        _, rc, _, ridx, _ = canonical.kmeans_fit(x[0, :, :n].float().numpy(), init.numpy(), iters)
+        assert np.array_equal(idx.cpu().numpy(), ridx)
+        assert np.array_equal(cent.cpu().numpy().view(np.int32), rc.view(np.int32))
+    err = (out.float().cpu() - ref.float()).abs()
+    print(f"[D=64] bits={bits}: max {err.max().item():.3e} mean {err.mean().item():.3e}", flush=True)
+    assert err.mean().item() <= 2e-3
+    assert err.max().item() <= 2e-2
