@@ -404,6 +404,8 @@ def measure(name, steps, warmup, stage_reps):
             ms = (time.perf_counter() - t0) * 1e3 / steps
         finally:
             attention_cuda.launch_events = None
+        if not launches:
+            raise RuntimeError("the layer step ran no work-list attention launch to time")
         t_attn = sum(a.elapsed_time(b) for a, b in launches) / len(launches)
         stages, flops, attn_args = stage_breakdown(layer, wl, q, k, v, q_init, k_init, stage_reps)
     value = flops / (ms * 1e-3) / 1e12
