@@ -512,7 +512,7 @@ def main():
         profile_target(args)
         return
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are not part of it",
+        print(json.dumps({"error": "bench.py measures one GPU; runs on more than one are not supported",
                           "n_gpus": args.gpus}))
         sys.exit(2)
     if args.sequence:

@@ -1,8 +1,9 @@
 """CPU oracle for the PECO per-layer attention hot path.
 
-TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() and by
-bench.py's cpu_baseline leg, always as the checker. The product package
-(peco_amd) never imports it.
+TEST INFRASTRUCTURE ONLY: imported by tests/ and __graft_entry__.smoke(), which check the
+GPU results against it, and by bench.py's cpu_baseline leg, which times it as the CPU
+baseline. The product package (peco_amd) never imports it, and no GPU figure is measured on
+it.
 
 Two layers:
 - ``oracle.canonical``: ctypes wrapper over ``peco_oracle.c``, the fixed-order

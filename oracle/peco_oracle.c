@@ -2,8 +2,9 @@
  * CPU oracle for the PECO per-layer attention hot path.
  *
  * TEST INFRASTRUCTURE ONLY. This file is compiled into oracle/_build/libpeco_oracle.so
- * and is loaded by tests/, by __graft_entry__.smoke() and by bench.py's cpu_baseline
- * leg, always as the checker. The product library (peco_amd) never links or calls it.
+ * and is loaded by tests/ and __graft_entry__.smoke(), which check the GPU results against
+ * it, and by bench.py's cpu_baseline leg, which times it as the CPU baseline. The product
+ * library (peco_amd) never links or calls it.
  *
  * Every function restates the reference algorithm with a fixed, documented fp32
  * operation order, so that the HIP kernels can be required to match it bit for bit:
