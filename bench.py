@@ -24,6 +24,7 @@ import argparse
 import json
 import math
 import os
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -84,10 +85,10 @@ def stage_breakdown(layer, wl, q, k, v, q_init, k_init, reps):
     """Per-stage device time (ms) with events on the current stream, and the realised FLOPs.
 
     The stages follow ``PecoAttention.attention``: the selection launch also writes the
-    attention's work list (kept-segment lists and ordered items). With Base-Offset off the
-    attention reads Q/K/V through the sort permutations; with it on, the fit's last update
-    also writes K (fake-quantized) and V in key-cluster order, and the attention reads Q
-    through the permutation and fake-quantizes it as it loads it, so there is no pack stage.
+    attention's work list (kept-segment lists and ordered items). The attention reads Q/K/V
+    through the sort permutations; with Base-Offset on, the fit's last update also writes K
+    fake-quantized in original order and the attention fake-quantizes Q as it loads it, so
+    there is no pack stage.
     """
     from peco_amd import clustering_cuda, workloads
 
@@ -101,9 +102,9 @@ def stage_breakdown(layer, wl, q, k, v, q_init, k_init, reps):
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
         ev[0].record()
         layer.q_centroids, layer.k_centroids = q_init, k_init
-        ql, kl, qs, ks = layer._update_cluster_state(q[:, :, :n], k[:, :, :n],
-                                                     pack_keys=(s.bits, k, v) if s.bits else None)
-        q_idx, k_idx = layer._last_fit
+        fit = layer._fit_clusters(q[:, :, :n], k[:, :, :n], pack_keys=(s.bits, k, None) if s.bits else None,
+                                  pack_order="original")
+        qs, ks, q_idx, k_idx = fit.q_sizes, fit.k_sizes, fit.q_idx, fit.k_idx
         ev[1].record()
         work = clustering_cuda.select_work(
             layer.q_centroids.reshape(1, heads, -1, dim), layer.k_centroids.reshape(1, heads, -1, dim), qs, ks,
@@ -112,8 +113,7 @@ def stage_breakdown(layer, wl, q, k, v, q_init, k_init, reps):
         if s.bits == 0:
             attn_args = (q, k, v, work, q_idx, k_idx, n, None, 0)
         else:
-            kp, vp = layer._last_pack
-            attn_args = (q, kp, vp, work, q_idx, None, n, layer.q_centroids, s.bits)
+            attn_args = (q, fit.pack[0], v, work, q_idx, k_idx, n, layer.q_centroids, s.bits)
         run_attention(attn_args)
         ev[3].record()
         torch.cuda.synchronize()
@@ -163,14 +163,32 @@ def measured_traffic(workload):
 
 
 def cpu_model():
-    """The host CPU's model name (as lscpu reports it)."""
+    """The host CPU's model name, as lscpu reports it, with family/model/stepping and clock
+    (a virtual machine may report only a generic name such as "AMD EPYC")."""
+    fields = {}
     try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
-    except OSError:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            key, _, value = line.partition(":")
+            fields[key.strip()] = value.strip()
+    except (OSError, subprocess.SubprocessError):
         pass
-    return "unknown"
+    if "Model name" not in fields:
+        try:
+            for line in open("/proc/cpuinfo"):
+                key, _, value = line.partition(":")
+                fields.setdefault({"model name": "Model name", "cpu family": "CPU family", "model": "Model",
+                                   "stepping": "Stepping", "cpu MHz": "CPU MHz"}.get(key.strip(), "_"), value.strip())
+        except OSError:
+            pass
+    name = fields.get("Model name", "unknown")
+    detail = [f"{k.lower()} {fields[k]}" for k in ("CPU family", "Model", "Stepping") if fields.get(k)]
+    mhz = fields.get("CPU max MHz") or fields.get("CPU MHz")
+    if mhz:
+        detail.append(f"{float(mhz):.0f} MHz")
+    if fields.get("Socket(s)"):
+        detail.append(f"{fields['Socket(s)']} socket(s)")
+    return f"{name} ({', '.join(detail)})" if detail else name
 
 
 def cpu_baseline(wl, budget_s):
@@ -268,8 +286,8 @@ def profile_target(args):
         if args.profile_target == "pack":
             # Stages 2+3: fake-quant Q/K against their centroids and gather Q/K/V into cluster order.
             layer.q_centroids, layer.k_centroids = wl.q_init, wl.k_init
-            ql, kl, _, _ = layer._update_cluster_state(wl.query[:, :, :n], wl.key[:, :, :n])
-            q_idx, k_idx = layer._last_fit
+            fit = layer._fit_clusters(wl.query[:, :, :n], wl.key[:, :, :n])
+            ql, kl, q_idx, k_idx = fit.q_labels, fit.k_labels, fit.q_idx, fit.k_idx
             pack_args = ([wl.query, wl.key, wl.value], [q_idx, k_idx, k_idx], [ql, kl, None],
                          [layer.q_centroids, layer.k_centroids, None], [s.bits, s.bits, 0], n)
             clustering_cuda.pack_clustered(*pack_args)
@@ -454,9 +472,9 @@ def measure_integer_scores(name, steps, warmup, reps):
         torch.cuda.synchronize()
         ms = (time.perf_counter() - t0) * 1e3 / steps
         layer.q_centroids, layer.k_centroids = wl.q_init, wl.k_init
-        _, _, qs, ks = layer._update_cluster_state(q[:, :, :n], k[:, :, :n], pack_keys=(s.bits, k, v, True))
-        q_idx, _ = layer._last_fit
-        kp, vp, codes, low, scale = layer._last_pack
+        fit = layer._fit_clusters(q[:, :, :n], k[:, :, :n], pack_keys=(s.bits, k, v, True))
+        qs, ks, q_idx = fit.q_sizes, fit.k_sizes, fit.q_idx
+        kp, vp, codes, low, scale = fit.pack
         minimum = math.ceil(wl.min_kc_ratio * s.num_k_centroids)
         qc4 = layer.q_centroids.reshape(1, heads, -1, dim)
         kc4 = layer.k_centroids.reshape(1, heads, -1, dim)

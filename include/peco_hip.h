@@ -86,20 +86,21 @@ int peco_kmeans_fit(int num_problems, const void* const* x, const int64_t* x_bat
 
 /* peco_kmeans_fit whose last update also packs (fuses peco/processor.py:141-149 into the
  * fit): for problem i with hat[i] non-null, hat[i] [batch, length, dims] receives x's rows
- * in the final cluster order, Base-Offset fake-quantized with bits[i] (4 or 8) against the
- * final centres, then x's rows [tokens, length) unchanged (the text; x_batch_stride[i] must
- * cover length rows); with_in[i] -> with_out[i] ([batch, length, dims], both or neither)
- * are gathered in the same order with their text rows copied. codes[i], low[i], scale[i]
- * (all three or none; uint8 [batch, tokens, dims], fp32 [batch, tokens]) receive the
- * Base-Offset payload of hat[i]'s first tokens rows in the same order, as
- * quantize_base_offset computes it (peco/quantization.py:97-128). Labels, centres, counts and
- * the permutation are those of peco_kmeans_fit. (ABI revision 4: codes/low/scale added.) */
+ * Base-Offset fake-quantized with bits[i] (4 or 8) against the final centres, in the final
+ * cluster order (hat_order 0) or each at its own token position (hat_order 1), then x's rows
+ * [tokens, length) unchanged (the text; x_batch_stride[i] must cover length rows);
+ * with_in[i] -> with_out[i] ([batch, length, dims], both or neither, hat_order 0 only) are
+ * gathered in the same order with their text rows copied. codes[i], low[i], scale[i] (all
+ * three or none; uint8 [batch, tokens, dims], fp32 [batch, tokens]) receive the Base-Offset
+ * payload of hat[i]'s first tokens rows in the same order, as quantize_base_offset computes
+ * it (peco/quantization.py:97-128). Labels, centres, counts and the permutation are those of
+ * peco_kmeans_fit. (ABI revision 4: codes/low/scale added; revision 5: hat_order.) */
 int peco_kmeans_fit_pack(int num_problems, const void* const* x, const int64_t* x_batch_stride,
                          const float* const* centers_in, float* const* centers_out, int32_t* const* labels,
                          int32_t* const* counts, int32_t* const* sorted_indices, int32_t* const* offsets,
                          const int* batch, const int* tokens, const int* clusters, int dims, int dtype, int iterations,
                          void* const* hat, const int* bits, const void* const* with_in, void* const* with_out,
-                         uint8_t* const* codes, float* const* low, float* const* scale, int length,
+                         uint8_t* const* codes, float* const* low, float* const* scale, int length, int hat_order,
                          void* workspace, size_t workspace_bytes, void* stream);
 
 /* Diagnostic of the certified assignment (no counterpart in the reference): for bf16 x
@@ -178,6 +179,9 @@ int peco_select_cluster_connections(const float* qc, const float* kc, const int3
 /* ABI revision 4 added peco_base_offset_attention and the codes/low/scale outputs of
  * peco_kmeans_fit_pack. */
 
+/* ABI revision 5 added the hat_order argument of peco_kmeans_fit_pack, q_centroids together
+ * with k_index in peco_sparse_attention_work, and made its work buffer writable. */
+
 /* int32 elements of peco_select_work's work buffer (bh entries, sq query rows, a cq(+2) x
  * ck(+2) map). */
 size_t peco_select_work_size(int bh, int sq, int cq, int ck, int extend);
@@ -205,14 +209,16 @@ int peco_select_work(const float* qc, const float* kc, const int32_t* q_counts, 
  * peco/kernels/sparse_attention.cu:210 with the work list precomputed). out_index and
  * k_index as in peco_sparse_attention_ex (k_index null: q/k/v in cluster order) and
  * peco_sparse_attention_indexed (out_index = q_index: q/k/v in original order). With
- * q_centroids (fp32 [bh, q_clusters, d], out_index given, k_index null) k and v are in
- * cluster order and q in original order: query row j < out_index_rows is read from row
- * out_index[j] and Base-Offset fake-quantized with `bits` (4 or 8) against the centroid of
- * its cluster as it is loaded (peco/processor.py:141 and the Q gather fused into the kernel;
- * the text rows' clusters, q_clusters and up, are not quantized). */
+ * q_centroids (fp32 [bh, q_clusters, d], out_index given) q is in original order: query row
+ * j < out_index_rows is read from row out_index[j] and Base-Offset fake-quantized with `bits`
+ * (4 or 8) against the centroid of its cluster as it is loaded (peco/processor.py:141 and the
+ * Q gather fused into the kernel; the text rows' clusters, q_clusters and up, are not
+ * quantized); k and v are then in cluster order (k_index null) or in original order read
+ * through k_index. The work buffer is written: the persistent grid's item queue counters live
+ * in it (every launch leaves them zero), so launches sharing one buffer must not overlap. */
 int peco_sparse_attention_work(const void* q, const void* k, const void* v, void* output, const int32_t* out_index,
                                int out_index_rows, const int32_t* k_index, const float* q_centroids, int q_clusters,
-                               int bits, const int32_t* work, size_t work_ints, int bh, int sq, int sk, int d, int cq,
+                               int bits, int32_t* work, size_t work_ints, int bh, int sq, int sk, int d, int cq,
                                int ck, int dtype, void* stream);
 
 /* Cluster-sparse attention with Base-Offset scores on the integer MFMA. No counterpart in the

@@ -126,8 +126,8 @@ SIGNATURES = {
     "peco_sparse_attention_indexed": (I, [P] * 9 + [I, P, P, Z] + [I] * 7 + [P]),
     "peco_select_cluster_connections": (I, [P] * 4 + [I] * 4 + [ctypes.c_float] + [I] * 4 + [P] * 5),
     "peco_sparse_attention_noalloc": (I, [P] * 7 + [I] * 7 + [P]),
-    "peco_kmeans_fit_pack": (I, [I, PP, P, PP, PP, PP, PP, PP, PP, IP, IP, IP, I, I, I, PP, IP, PP, PP, PP, PP, PP, I, P,
-                                 Z, P]),
+    "peco_kmeans_fit_pack": (I, [I, PP, P, PP, PP, PP, PP, PP, PP, IP, IP, IP, I, I, I, PP, IP, PP, PP, PP, PP, PP, I, I,
+                                 P, Z, P]),
     "peco_select_work_size": (Z, [I] * 5),
     "peco_select_work": (I, [P] * 4 + [I] * 4 + [ctypes.c_float] + [I] * 6 + [P] * 4 + [Z, P]),
     "peco_sparse_attention_work": (I, [P] * 5 + [I, P, P, I, I, P, Z] + [I] * 7 + [P]),

@@ -197,9 +197,10 @@ def sparse_attention_work(
     ``out_index_rows`` output rows); with it, Q/K/V are in original order and read through
     ``out_index`` (queries, also the output scatter) and ``k_index`` (keys and values), as
     ``sparse_attention_indexed``. With ``q_centroids`` (fp32 [B*H, CQ, D]; needs
-    ``out_index``, no ``k_index``) K/V are in cluster order and Q in original order, read
-    through ``out_index`` and Base-Offset fake-quantized with ``bits`` against its cluster's
-    centroid as it is loaded (peco/processor.py:141 and the Q gather fused into the kernel).
+    ``out_index``) Q is in original order, read through ``out_index`` and Base-Offset
+    fake-quantized with ``bits`` against its cluster's centroid as it is loaded
+    (peco/processor.py:141 and the Q gather fused into the kernel); K/V are then in cluster
+    order, or in original order read through ``k_index`` when it is given.
     """
     for name, t in (("q", q), ("k", k), ("v", v)):
         if not isinstance(t, torch.Tensor) or not t.is_cuda or not t.is_contiguous() or t.dim() != 4:
@@ -212,6 +213,9 @@ def sparse_attention_work(
         raise ValueError("q/k/v shapes must be [B,H,S,D] with D in {64, 128} and matching K/V")
     if work.bh != batch * heads or work.sq != sq or work.sk != sk:
         raise ValueError("the work list was built for another shape")
+    if not work.valid():
+        raise RuntimeError("the work list was overwritten by a later select_work call of the same shape on this "
+                           "stream; call select_work again")
     output = torch.empty_like(q)
     if sq == 0:
         return output
@@ -226,8 +230,8 @@ def sparse_attention_work(
         _check_index(k_index, "k_index", batch, heads, rows)
     q_clusters = 0
     if q_centroids is not None:
-        if out_index is None or k_index is not None or bits not in (4, 8):
-            raise ValueError("q_centroids needs out_index, no k_index and bits in {4, 8}")
+        if out_index is None or bits not in (4, 8):
+            raise ValueError("q_centroids needs out_index and bits in {4, 8}")
         if q_centroids.dtype != torch.float32 or not q_centroids.is_contiguous() or q_centroids.dim() != 3 \
                 or q_centroids.shape[0] != batch * heads or q_centroids.shape[2] != dim \
                 or not 1 <= q_centroids.shape[1] <= work.rows or q_centroids.device != q.device:

@@ -7,6 +7,7 @@ Every call is asynchronous on torch's current stream.
 """
 from __future__ import annotations
 
+import collections
 import ctypes
 
 import torch
@@ -129,7 +130,7 @@ class KMeansProblem:
         self.clusters = self.init.shape[1]
 
 
-def kmeans_fit(problems, iterations, pack=None):
+def kmeans_fit(problems, iterations, pack=None, pack_order="cluster"):
     """Fused Lloyd fit of one or two problems in shared launches.
 
     Returns, per problem, (labels int32 [B,N], centers fp32 [B,K,D], counts int32 [B,K],
@@ -145,6 +146,10 @@ def kmeans_fit(problems, iterations, pack=None):
     Base-Offset payload of hat's first N rows in that order: packed[i] = (hat, with_out,
     codes uint8 [B, N, D], low fp32 [B, N], scale fp32 [B, N]), the values
     quantize_base_offset computes (peco/quantization.py:97-128).
+
+    ``pack_order="original"`` writes hat's rows [0, N) (and the payload) at each token's own
+    position instead of in cluster order, so hat is x with its video rows fake-quantized;
+    no ``with_tensor`` is gathered then.
     """
     library = _library()
     if not 1 <= len(problems) <= 2:
@@ -156,6 +161,8 @@ def kmeans_fit(problems, iterations, pack=None):
         raise ValueError("kmeans_fit problems must share dims, dtype and device")
     if pack is not None and len(pack) != len(problems):
         raise ValueError("pack needs one entry per problem")
+    if pack_order not in ("cluster", "original"):
+        raise ValueError("pack_order must be 'cluster' or 'original'")
     outs = []
     ws_bytes = 0
     for p in problems:
@@ -202,6 +209,8 @@ def kmeans_fit(problems, iterations, pack=None):
             raise ValueError("x's batch stride must cover the packed length")
         hats.append(torch.empty((p.batch, length, dims), dtype=dtype, device=dev))
         if w is not None:
+            if pack_order != "cluster":
+                raise ValueError("a gathered companion needs pack_order='cluster'")
             if w.shape != (p.batch, length, dims) or w.dtype != dtype or not w.is_contiguous() or w.device != dev:
                 raise ValueError("the gathered companion must be a contiguous [B, length, D] tensor like x")
             withs_out.append(torch.empty_like(w))
@@ -218,7 +227,7 @@ def kmeans_fit(problems, iterations, pack=None):
         status = library.peco_kmeans_fit_pack(
             *common, _native.ptr_array(hats), _native.int_array(bits), _native.ptr_array(withs_in),
             _native.ptr_array(withs_out), _native.ptr_array(codes), _native.ptr_array(lows),
-            _native.ptr_array(scales), int(length or 0), _native.ptr(ws), ws_bytes,
+            _native.ptr_array(scales), int(length or 0), int(pack_order == "original"), _native.ptr(ws), ws_bytes,
             _retain_on_current_stream(dev, *tensors, *extra))
     _raise_cluster_error(status)
     packed = [None if h is None else ((h, w) if q is None else (h, w, *q))
@@ -271,10 +280,20 @@ class SelectionWork:
     """Work list of one peco_select_work launch: the kept-segment list of every map row and
     the attention items of every (batch, head) in cost order, in ``buffer`` (int32). ``rows``
     and ``cols`` are the map's dimensions (text groups included), ``sq``/``sk`` the attention's
-    query/key lengths it was built for."""
+    query/key lengths it was built for.
 
-    def __init__(self, buffer, bh, sq, sk, rows, cols, ints):
+    Calls of ``select_work`` of one shape on one stream share a cached buffer, so a
+    SelectionWork stays valid only until the next such call: ``sparse_attention_work``
+    checks ``valid()`` and raises for a work list that a later call has overwritten."""
+
+    def __init__(self, buffer, bh, sq, sk, rows, cols, ints, slot=None):
         self.buffer, self.bh, self.sq, self.sk, self.rows, self.cols, self.ints = buffer, bh, sq, sk, rows, cols, ints
+        self._slot = slot
+        self._generation = None if slot is None else slot.generation
+
+    def valid(self):
+        """False once a later select_work call has rewritten this work list's buffer."""
+        return self._slot is None or self._slot.generation == self._generation
 
     def _layout(self):
         b, re, ce = self.bh, self.rows, self.cols
@@ -312,19 +331,33 @@ class SelectionWork:
         return self.buffer[head:head + b * re * (ce + 2) * 2].view(b, re, ce + 2, 2)
 
 
-# One work buffer per (device, stream, shape): its arrival counters start at zero and every
-# launch leaves them zero, and launches on one stream are ordered, so they can share it.
-_WORK_BUFFERS = {}
+class _WorkSlot:
+    """A cached work buffer and the number of select_work launches that have written it."""
+
+    def __init__(self, buffer):
+        self.buffer = buffer
+        self.generation = 0
 
 
-def _work_buffer(device, ints, shape):
+# Work buffers by (device, stream, shape): their arrival and queue counters start at zero and
+# every launch leaves them zero, and launches on one stream are ordered, so they can share a
+# buffer. The least recently used entries beyond the limit are dropped (a SelectionWork keeps
+# its own buffer alive).
+_WORK_BUFFERS = collections.OrderedDict()
+_WORK_BUFFER_LIMIT = 8
+
+
+def _work_slot(device, ints, shape):
     stream = torch.cuda.current_stream(device).cuda_stream
     key = (device.index, stream, shape)
-    buf = _WORK_BUFFERS.get(key)
-    if buf is None:
-        buf = torch.zeros(ints, dtype=torch.int32, device=device)
-        _WORK_BUFFERS[key] = buf
-    return buf
+    slot = _WORK_BUFFERS.pop(key, None)
+    if slot is None:
+        slot = _WorkSlot(torch.zeros(ints, dtype=torch.int32, device=device))
+    _WORK_BUFFERS[key] = slot
+    while len(_WORK_BUFFERS) > _WORK_BUFFER_LIMIT:
+        _WORK_BUFFERS.popitem(last=False)
+    slot.generation += 1
+    return slot
 
 
 def select_work(query_centroids, key_centroids, q_counts, k_counts, p, minimum, text, sq, sk):
@@ -333,7 +366,8 @@ def select_work(query_centroids, key_centroids, q_counts, k_counts, p, minimum, 
     Same inputs as ``select_connections`` with ``text=(valid_text, text_length)`` or None;
     sq/sk are the attention's query/key lengths (video + text). No map is written: the
     attention reads each query cluster's kept-segment list instead. Returns a
-    ``SelectionWork`` for ``attention_cuda.sparse_attention_work``.
+    ``SelectionWork`` for ``attention_cuda.sparse_attention_work``, valid until the next
+    ``select_work`` call of the same shape on the same stream (which reuses its buffer).
     """
     library = _library()
     lead = query_centroids.shape[:-2]
@@ -354,13 +388,14 @@ def select_work(query_centroids, key_centroids, q_counts, k_counts, p, minimum, 
     if ints == 0:
         raise ValueError("invalid selection work shape")
     with torch.cuda.device(dev):
-        work = _work_buffer(dev, ints, (bh, int(sq), re, ce))
+        slot = _work_slot(dev, ints, (bh, int(sq), re, ce))
+        work = slot.buffer
         status = library.peco_select_work(
             _native.ptr(qc), _native.ptr(kc), _native.ptr(qn), _native.ptr(kn), bh, cq, ck, dims, float(p),
             int(minimum), int(extend), int(valid_text), int(text_length), int(sq), int(sk), None, None, None,
             _native.ptr(work), ints, _retain_on_current_stream(dev, qc, kc, qn, kn, work))
     _raise_cluster_error(status)
-    return SelectionWork(work, bh, int(sq), int(sk), re, ce, ints)
+    return SelectionWork(work, bh, int(sq), int(sk), re, ce, ints, slot)
 
 
 def pack_clustered(tensors, indices, labels, centroids, bits, video):

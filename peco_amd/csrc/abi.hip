@@ -22,4 +22,4 @@ PECO_API const char* peco_cluster_error_message(int code) { return peco_status(c
 
 PECO_API const char* peco_attention_error_string(int code) { return peco_status(code); }
 
-PECO_API int peco_abi_version(void) { return 4; }
+PECO_API int peco_abi_version(void) { return 5; }

@@ -327,11 +327,14 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 //   kQuantQ: K and V in cluster order, Q in original order read through out_index as in
 //     kIndexed and Base-Offset fake-quantized as it is loaded: every row of an item belongs
 //     to its query cluster qc, so rows of a video cluster (qc < qcent_rows) take centroid
-//     qcent[bh, qc] and levels = 2^bits - 1 (peco/processor.py:141, fused into the load).
+//     qcent[bh, qc] and levels = 2^bits - 1 (peco/processor.py:141, fused into the load);
+//   kIndexedQuantQ: Q as in kQuantQ, K and V in original order read through k_index as in
+//     kIndexed (the Base-Offset layer: K fake-quantized in original order by the fit, V the
+//     caller's own tensor).
 // The key stream of an item comes either from a kept-segment list (segs, as the selection
 // launch writes it: {count n, stream length L}, n segments, sentinel per map row) or, when segs
 // is null, from the item's map row and the clamped key-cluster prefix kprefix [bh, ck + 1].
-enum InputMode : int { kPacked = 0, kIndexed = 1, kQuantQ = 2 };
+enum InputMode : int { kPacked = 0, kIndexed = 1, kQuantQ = 2, kIndexedQuantQ = 3 };
 
 // One work item (linear index g over bands x slots x heads, see below) of the attention.
 template <int DT, int D, int kMode>
@@ -342,7 +345,8 @@ __device__ __forceinline__ void attention_item(
     const int32_t* __restrict__ out_index, int oi_rows, const int32_t* __restrict__ k_index,
     const float* __restrict__ qcent, int qcent_rows, float levels, int bhn, int band, int sq, int sk, int cq,
     int ck, float scale_log2) {
-    constexpr bool kIndexedKV = kMode == kIndexed;
+    constexpr bool kIndexedKV = kMode == kIndexed || kMode == kIndexedQuantQ;
+    constexpr bool kQuantLoad = kMode == kQuantQ || kMode == kIndexedQuantQ;
     using T = Tiles<D>;
     constexpr int S = D / 16;       // k-steps of S^T over channels
     constexpr int NB = D / 32;      // 32-channel blocks of O^T
@@ -418,8 +422,8 @@ __device__ __forceinline__ void attention_item(
     }
     // kQuantQ: the centroid channels of this lane's half row (every row of the item has the
     // item's query cluster), requested with the rows.
-    f32x8 qc_row[kMode == kQuantQ ? S : 1];
-    if constexpr (kMode == kQuantQ) {
+    f32x8 qc_row[kQuantLoad ? S : 1];
+    if constexpr (kQuantLoad) {
         const float* crow = qcent + (head * qcent_rows + min(qc, qcent_rows - 1)) * D + 8 * h;
 #pragma unroll
         for (int s = 0; s < S; ++s) qc_row[s] = *reinterpret_cast<const f32x8*>(crow + 16 * s);
@@ -622,7 +626,7 @@ __device__ __forceinline__ void attention_item(
             }
         }
     };
-    if constexpr (kMode == kQuantQ) {
+    if constexpr (kQuantLoad) {
         // The query rows and centroid must arrive before the tile loads below are issued: the
         // compiler does not count those loads, so a later wait for the rows would also wait
         // for the tile.
@@ -633,7 +637,7 @@ __device__ __forceinline__ void attention_item(
     }
     __syncthreads();
     if (ntiles > 0) load_tile_lds<D, 4>(ks[0], vs[0], kh, vh, prow[0], wave, lane);
-    if constexpr (kMode == kQuantQ) {
+    if constexpr (kQuantLoad) {
         if (qc < qcent_rows) {
             // This lane holds channels 16s + 8h .. +7 of its row and lane l ^ 32 the others:
             // the row's residual bounds are the two lanes' bounds combined. All of it is VALU
@@ -1308,7 +1312,8 @@ int attention_head_band(int bh, int sk, int d) {
 }
 
 // Launch of the attention kernel over a built work list (map + kprefix, or segs).
-// q_centroids (nullable, with out_index and no k_index) selects the kQuantQ input mode.
+// q_centroids (nullable, with out_index) selects the kQuantQ input mode, or kIndexedQuantQ
+// with k_index.
 // Compute units of the current device (cached per device).
 int device_compute_units() {
     static std::mutex m;
@@ -1335,7 +1340,7 @@ int launch_attention_kernel(const void* q, const void* k, const void* v, const u
                             int cap, void* output, const int32_t* out_index, int out_index_rows,
                             const int32_t* k_index, const float* q_centroids, int q_clusters, int bits, int bh,
                             int sq, int sk, int d, int cq, int ck, int dtype, int32_t* queues, hipStream_t s) {
-    const int mode = k_index ? kIndexed : (q_centroids ? kQuantQ : kPacked);
+    const int mode = k_index ? (q_centroids ? kIndexedQuantQ : kIndexed) : (q_centroids ? kQuantQ : kPacked);
     const float levels = static_cast<float>((1 << bits) - 1);
     const size_t lds_attn = sizeof(int) * 2 * (static_cast<size_t>(ck) + 1);
     const float scale_log2 = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(d)));
@@ -1366,6 +1371,7 @@ int launch_attention_kernel(const void* q, const void* k, const void* v, const u
     do {                                                                                                           \
         if (mode == kIndexed) PECO_ATTN_D(DT_, kIndexed);                                                          \
         else if (mode == kQuantQ) PECO_ATTN_D(DT_, kQuantQ);                                                       \
+        else if (mode == kIndexedQuantQ) PECO_ATTN_D(DT_, kIndexedQuantQ);                                         \
         else PECO_ATTN_D(DT_, kPacked);                                                                            \
     } while (0)
     if (dtype == kBF16) PECO_ATTN_M(kBF16);
@@ -1441,23 +1447,26 @@ PECO_API int peco_sparse_attention_indexed(const void* q, const void* k, const v
 // bh, sq and map dims cq x ck), so no builder runs and no map row is read. Q/K/V addressing
 // and out_index/k_index are those of peco_sparse_attention_ex (k_index null) and
 // peco_sparse_attention_indexed (out_index = q_index, k_index given). With q_centroids
-// (fp32 [bh, q_clusters, d]; needs out_index and no k_index) K and V are in cluster order and
-// Q in original order: query row j < out_index_rows is read from row out_index[j] and
-// Base-Offset fake-quantized with `bits` against its cluster's centroid as it is loaded.
+// (fp32 [bh, q_clusters, d]; needs out_index) Q is in original order: query row
+// j < out_index_rows is read from row out_index[j] and Base-Offset fake-quantized with `bits`
+// against its cluster's centroid as it is loaded; K and V are then in cluster order, or in
+// original order read through k_index when it is given. The work buffer is written: the
+// persistent grid takes items with atomic counters in it (left zero at the end), so two
+// launches sharing one work buffer must not overlap.
 PECO_API int peco_sparse_attention_work(const void* q, const void* k, const void* v, void* output,
                                         const int32_t* out_index, int out_index_rows, const int32_t* k_index,
-                                        const float* q_centroids, int q_clusters, int bits, const int32_t* work,
+                                        const float* q_centroids, int q_clusters, int bits, int32_t* work,
                                         size_t work_ints, int bh, int sq, int sk, int d, int cq, int ck, int dtype,
                                         void* stream) {
     if (!q || !k || !v || !output || !work || bh < 1 || bh > 65535 || sq < 0 || sk < 0 || cq < 1 || ck < 1 ||
         (d != 64 && d != 128) || (dtype != kF16 && dtype != kBF16) ||
         (out_index && (out_index_rows < 0 || out_index_rows > sq)) || (k_index && (!out_index || out_index_rows > sk)) ||
-        (q_centroids && (!out_index || k_index || q_clusters < 1 || q_clusters > cq || (bits != 4 && bits != 8))))
+        (q_centroids && (!out_index || q_clusters < 1 || q_clusters > cq || (bits != 4 && bits != 8))))
         return kInvalidValue;
     if (sq == 0) return kOk;
     if (work_ints < sel_work_ints(bh, sq, cq, ck)) return kWorkspaceTooSmall;
     if (sizeof(int) * 2 * (static_cast<size_t>(ck) + 1) > 24 * 1024) return kUnsupportedShape;
-    const SelWork W = sel_work_layout(const_cast<int32_t*>(work), bh, sq, cq, ck);
+    const SelWork W = sel_work_layout(work, bh, sq, cq, ck);
     return launch_attention_kernel(q, k, v, nullptr, nullptr, W.segs, W.counts, W.items, W.cap, output, out_index,
                                    out_index_rows, k_index, q_centroids, q_centroids ? q_clusters : 0,
                                    q_centroids ? bits : 0, bh, sq, sk, d, cq, ck, dtype, W.queues,

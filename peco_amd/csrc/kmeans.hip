@@ -70,6 +70,8 @@ struct KmProblem {
     // batch stride); with_in/with_out (nullable, [batch, length, D]) are gathered alike
     // without quantization. codes/low/scale (nullable together, [batch, tokens, D] uint8 and
     // [batch, tokens] fp32) receive the packed rows' Base-Offset payload in the same order.
+    // hat_order 1 writes every row at its own token position instead (original order; no
+    // with_in/with_out then), so hat is x with its video rows fake-quantized.
     void* hat;
     const void* with_in;
     void* with_out;
@@ -78,6 +80,7 @@ struct KmProblem {
     float* scale;
     int hat_bits;
     int length;
+    int hat_order;
 };
 
 constexpr int kMaxKm = 2;
@@ -816,10 +819,11 @@ __device__ __forceinline__ int km_update_problem(const KmArgs& a, int block) {
     return p;
 }
 
-// Packing pass of the last update: the members of one cluster, in sorted order m (= their
-// packed row), 16 lanes per row (8 channels each; 8 lanes at D = 64). The members go 64 at
-// a time (`first`, `stride`: this wavefront's first member and step); one index load per
-// lane, then the rows of 8 passes (32 or 64 rows) are requested together before any is used.
+// Packing pass of the last update: the members of one cluster, in sorted order m (their
+// packed row, or with P.hat_order their own token row), 16 lanes per row (8 channels each; 8
+// lanes at D = 64). The members go 64 at a time (`first`, `stride`: this wavefront's first
+// member and step); one index load per lane, then the rows of 8 passes (32 or 64 rows) are
+// requested together before any is used.
 template <int DT> struct Raw8 {
     u32x4 v[DT == kF32 ? 2 : 1];
     __device__ __forceinline__ void load(const void* base, int64_t e) {
@@ -834,7 +838,8 @@ template <int DT> struct Raw8 {
     }
 };
 
-template <int DT, int D>
+// kOriginal: rows go to their own token positions (P.hat_order 1), with no companion tensor.
+template <int DT, int D, bool kOriginal>
 __device__ __forceinline__ void pack_members(const KmProblem& P, int b, int begin, int end, const float* centre,
                                              int first, int stride) {
     constexpr int G = D / 8;       // lanes per row
@@ -845,7 +850,7 @@ __device__ __forceinline__ void pack_members(const KmProblem& P, int b, int begi
     const int sub = lane % G, rsub = lane / G;
     const int32_t* idx = P.indices + static_cast<int64_t>(b) * P.tokens;
     const float levels = static_cast<float>((1 << P.hat_bits) - 1);
-    const bool with = P.with_out != nullptr;
+    const bool with = !kOriginal && P.with_out != nullptr;
     float c[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) c[i] = centre[sub * 8 + i];
@@ -854,13 +859,17 @@ __device__ __forceinline__ void pack_members(const KmProblem& P, int b, int begi
         const int mine = idx[m0 + min(lane, cnt - 1)];
         for (int u0 = 0; u0 < PASSES && u0 * R < cnt; u0 += U) {
             float xv[U][8];
-            Raw8<DT> wv[U];
+            Raw8<DT> wv[kOriginal ? 1 : U];
+            int toks[kOriginal ? U : 1];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int r = min((u0 + u) * R + rsub, cnt - 1);  // clamped: every load is unconditional
                 const int tok = __shfl(mine, r, kWave);
+                if constexpr (kOriginal) toks[u] = tok;
                 Row8<DT>::load(P.x, b * P.x_stride + static_cast<int64_t>(tok) * D + sub * 8, xv[u]);
-                if (with) wv[u].load(P.with_in, (static_cast<int64_t>(b) * P.length + tok) * D + sub * 8);
+                if constexpr (!kOriginal) {
+                    if (with) wv[u].load(P.with_in, (static_cast<int64_t>(b) * P.length + tok) * D + sub * 8);
+                }
             }
 #pragma unroll
             for (int u = 0; u < U; ++u) {
@@ -869,11 +878,14 @@ __device__ __forceinline__ void pack_members(const KmProblem& P, int b, int begi
                 uint8_t q[8];
                 base_offset_lane<G>(xv[u], c, levels, out, q, lo, sc);
                 if (r < cnt) {
-                    const int64_t dst = (static_cast<int64_t>(b) * P.length + m0 + r) * D + sub * 8;
+                    const int pos = kOriginal ? toks[kOriginal ? u : 0] : m0 + r;
+                    const int64_t dst = (static_cast<int64_t>(b) * P.length + pos) * D + sub * 8;
                     Row8<DT>::store(P.hat, dst, out);
-                    if (with) wv[u].store(P.with_out, dst);
+                    if constexpr (!kOriginal) {
+                        if (with) wv[u].store(P.with_out, dst);
+                    }
                     if (P.codes) {
-                        const int64_t row = static_cast<int64_t>(b) * P.tokens + m0 + r;
+                        const int64_t row = static_cast<int64_t>(b) * P.tokens + pos;
                         u32x2 packed;
                         packed[0] = q[0] | (q[1] << 8) | (q[2] << 16) | (static_cast<uint32_t>(q[3]) << 24);
                         packed[1] = q[4] | (q[5] << 8) | (q[6] << 16) | (static_cast<uint32_t>(q[7]) << 24);
@@ -911,7 +923,9 @@ __device__ __forceinline__ void pack_text_rows(const KmArgs& a, int block) {
     }
 }
 
-template <int DT, int D, bool kPack = false>
+// kPack: 0 plain update; 1 the last update of a packing fit in cluster order, 2 in original
+// order (P.hat_order 1; every packing problem of the launch has the same order).
+template <int DT, int D, int kPack = 0>
 __global__ __launch_bounds__(kUpdateWaves * kWave) void km_update_kernel(KmArgs a, KmIter it) {
     constexpr int PER = D / kWave;  // channels per lane (1 or 2)
     __shared__ float row[kUpdateWaves][D];
@@ -975,7 +989,7 @@ __global__ __launch_bounds__(kUpdateWaves * kWave) void km_update_kernel(KmArgs 
                 if (P.hat) {
                     // The other wavefronts pack with wave 0 once it has left the centre in row[0].
                     __syncthreads();
-                    pack_members<DT, D>(P, b, begin, end, row[0], kWave * wave, kWave * kUpdateWaves);
+                    pack_members<DT, D, kPack == 2>(P, b, begin, end, row[0], kWave * wave, kWave * kUpdateWaves);
                 }
             }
             return;
@@ -1007,9 +1021,9 @@ __global__ __launch_bounds__(kUpdateWaves * kWave) void km_update_kernel(KmArgs 
         if (P.hat) {
             if (shared) {
                 __syncthreads();  // row[0] (this wavefront's centre) is published to the others
-                pack_members<DT, D>(P, b, begin, end, row[0], 0, kWave * kUpdateWaves);
+                pack_members<DT, D, kPack == 2>(P, b, begin, end, row[0], 0, kWave * kUpdateWaves);
             } else {
-                pack_members<DT, D>(P, b, begin, end, row[wave], 0, kWave);
+                pack_members<DT, D, kPack == 2>(P, b, begin, end, row[wave], 0, kWave);
             }
         }
     }
@@ -1131,8 +1145,13 @@ hipError_t run_fit(KmArgs& a, const KmIter* iters, int iterations, SortArgs sa, 
         }
         hipError_t e = launch_cluster_sort(sa, s, false);
         if (e != hipSuccess) return e;
-        if (i + 1 == iterations && a.text_blocks > 0)
-            hipLaunchKernelGGL((km_update_kernel<DT, D, true>), dim3(a.total_upd_blocks + a.text_blocks),
+        bool original = false;
+        for (int q = 0; q < a.num; ++q) original = original || (a.p[q].hat && a.p[q].hat_order);
+        if (i + 1 == iterations && a.text_blocks > 0 && original)
+            hipLaunchKernelGGL((km_update_kernel<DT, D, 2>), dim3(a.total_upd_blocks + a.text_blocks),
+                               dim3(kUpdateWaves * kWave), 0, s, a, iters[i]);
+        else if (i + 1 == iterations && a.text_blocks > 0)
+            hipLaunchKernelGGL((km_update_kernel<DT, D, 1>), dim3(a.total_upd_blocks + a.text_blocks),
                                dim3(kUpdateWaves * kWave), 0, s, a, iters[i]);
         else
             hipLaunchKernelGGL((km_update_kernel<DT, D>), dim3(a.total_upd_blocks), dim3(kUpdateWaves * kWave), 0, s,
@@ -1177,6 +1196,7 @@ struct KmFitDesc {
     float* scale = nullptr;
     int hat_bits = 0;
     int length = 0;
+    int hat_order = 0;
 };
 
 // Workspace (bytes) for one problem.
@@ -1252,6 +1272,7 @@ hipError_t km_fit(const KmFitDesc* descs, int num, int dims, int dtype, int iter
         P.scale = d.scale;
         P.hat_bits = d.hat_bits;
         P.length = d.length;
+        P.hat_order = d.hat_order;
         if (d.hat) {
             // Text copies: one 16-byte chunk per thread and row, at most 64 workgroups.
             const int64_t chunks = static_cast<int64_t>(d.batch) * std::max(d.length - d.tokens, 0) * (dims / 8);
@@ -1363,24 +1384,25 @@ PECO_API int peco_kmeans_fit(int num_problems, const void* const* x, const int64
 
 // peco_kmeans_fit whose last update also packs (fuses peco/processor.py:141-149 for the
 // problems given a hat): problem i with hat[i] writes hat[i] [batch, length, dims] (rows
-// [0, tokens) = x's rows in the final cluster order, Base-Offset fake-quantized with bits[i]
-// against the final centres; rows [tokens, length) = x's rows there, so x_batch_stride[i]
-// must cover length rows), and with_in[i] -> with_out[i] ([batch, length, dims], nullable)
-// gathered in the same order with its text rows copied. codes[i], low[i] and scale[i]
-// (nullable together; uint8 [batch, tokens, dims], fp32 [batch, tokens]) receive the codes,
-// row lows and row scales of hat[i]'s rows [0, tokens), as peco_base_offset_encode writes
-// them (peco/quantization.py:97-128), in the same cluster order.
+// [0, tokens) = x's rows Base-Offset fake-quantized with bits[i] against the final centres,
+// in the final cluster order, or with hat_order 1 each at its own token position; rows
+// [tokens, length) = x's rows there, so x_batch_stride[i] must cover length rows), and
+// with_in[i] -> with_out[i] ([batch, length, dims], nullable, cluster order only) gathered in
+// the same order with its text rows copied. codes[i], low[i] and scale[i] (nullable together;
+// uint8 [batch, tokens, dims], fp32 [batch, tokens]) receive the codes, row lows and row
+// scales of hat[i]'s rows [0, tokens), as peco_base_offset_encode writes them
+// (peco/quantization.py:97-128), in the same order.
 PECO_API int peco_kmeans_fit_pack(int num_problems, const void* const* x, const int64_t* x_batch_stride,
                                   const float* const* centers_in, float* const* centers_out, int32_t* const* labels,
                                   int32_t* const* counts, int32_t* const* sorted_indices, int32_t* const* offsets,
                                   const int* batch, const int* tokens, const int* clusters, int dims, int dtype,
                                   int iterations, void* const* hat, const int* bits, const void* const* with_in,
                                   void* const* with_out, uint8_t* const* codes, float* const* low,
-                                  float* const* scale, int length, void* workspace, size_t workspace_bytes,
-                                  void* stream) {
+                                  float* const* scale, int length, int hat_order, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
     if (num_problems < 1 || num_problems > kMaxKm || iterations < 1 || (dims != 64 && dims != 128) ||
         (dtype != kBF16 && dtype != kF16 && dtype != kF32) || !workspace || !hat || !bits || !with_in || !with_out ||
-        !codes || !low || !scale)
+        !codes || !low || !scale || (hat_order != 0 && hat_order != 1))
         return kInvalidValue;
     KmFitDesc d[kMaxKm];
     size_t need = 0;
@@ -1398,6 +1420,8 @@ PECO_API int peco_kmeans_fit_pack(int num_problems, const void* const* x, const 
             d[i].with_in = with_in[i];
             d[i].with_out = with_out[i];
             d[i].length = length;
+            d[i].hat_order = hat_order;
+            if (hat_order && with_in[i]) return kInvalidValue;
             if (!codes[i] != !low[i] || !codes[i] != !scale[i]) return kInvalidValue;
             d[i].codes = codes[i];
             d[i].low = low[i];

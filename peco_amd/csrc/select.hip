@@ -383,18 +383,20 @@ __global__ __launch_bounds__(kSelWaves * kWave) void select_kernel(
                 __hip_atomic_store(work.row_keys + static_cast<int64_t>(b) * re + r, rk, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
         }
-        // Arrival. The row lengths are the only data the last workgroup reads from the others:
-        // they are device-coherent stores (no L2 write-back needed), complete before the
-        // barrier, so they precede this workgroup's counter increment; the last workgroup reads
-        // them with device-coherent loads. The segment lists and items reach the attention
-        // through the kernel boundary.
+        // Arrival. The row lengths are the only data the last workgroup reads from the others
+        // (device-coherent stores and loads); the segment lists and items reach the attention
+        // through the kernel boundary. The barrier orders every wavefront's stores before the
+        // counter increment, a release at agent scope, and the last workgroup acquires before
+        // it reads, so the hand-over holds under the memory model, not only on the hardware's
+        // in-order completion of the stores.
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         if (threadIdx.x == 0)
-            last = __hip_atomic_fetch_add(work.tickets + b, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            last = __hip_atomic_fetch_add(work.tickets + b, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT) ==
                    groups - 1;
         __syncthreads();
         if (!last) return;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         // Last workgroup of entry b: clamped query offsets of the extended partition and the
         // stream length of every row, then the entry's items in cost order.
         int* qoff = reinterpret_cast<int*>(smem);  // [re + 1]

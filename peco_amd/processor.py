@@ -1,14 +1,16 @@
 """HunyuanVideo attention processor with PECO cluster-sparse attention (peco/processor.py interface).
 
-The sparse path of ``PecoAttention.attention`` runs as four groups of device launches:
+The sparse path of ``PecoAttention.attention`` runs as three groups of device launches:
   1. fused Q+K k-means (clustering_cuda.kmeans_fit): labels, centres, sizes and the
-     stable cluster permutation of both tensors;
-  2. one selection launch: cluster-pair map with the text partition appended
-     (select_cluster_connections + extend_text_partition);
-  3. one pack launch that fake-quantizes Q/K (Base-Offset, when enabled), gathers Q/K/V
-     into cluster order and appends the text rows (no slice copies, no concatenations);
-  4. the HIP work-list builder and MFMA sparse attention, whose epilogue writes every
-     video row straight back to its original sequence position.
+     stable cluster permutation of both tensors. With Base-Offset on, the last update also
+     writes K fake-quantized against its final centre, row for row in original order;
+  2. one selection launch (clustering_cuda.select_work): cluster-pair selection with the
+     text partition appended, each query cluster's kept key segments and the attention's
+     cost-ordered work items;
+  3. the MFMA sparse attention, which reads Q, K (or its fake-quantized copy) and V through
+     the sort permutations, fake-quantizes Q as it loads it when Base-Offset is on, and
+     writes every video row straight back to its original sequence position.
+No packed Q/K/V copies and no concatenations are made.
 """
 from __future__ import annotations
 
@@ -93,20 +95,6 @@ def extend_text_partition(dynamic_map, q_sizes, k_sizes, valid_text, text_length
     )
 
 
-def _extend_partition_on_device(dynamic_map, q_sizes, k_sizes, valid_text, text_length):
-    """extend_text_partition without the host-to-device copy of the two extra sizes."""
-    dynamic_map = F.pad(dynamic_map, (0, 2, 0, 2), value=False)
-    dynamic_map[..., -2, :-1] = True
-    dynamic_map[..., :-1, -2] = True
-    dynamic_map[..., -1, -1] = True
-    lead = q_sizes.shape[:-1]
-    extra = torch.empty((*lead, 2), dtype=torch.int32, device=q_sizes.device)
-    extra[..., 0] = valid_text
-    extra[..., 1] = text_length - valid_text
-    return (dynamic_map.contiguous(), torch.cat((q_sizes.to(torch.int32), extra), -1).contiguous(),
-            torch.cat((k_sizes.to(torch.int32), extra), -1).contiguous())
-
-
 def _rotary_function():
     """diffusers' apply_rotary_emb when diffusers is installed, else the restatement below."""
     try:
@@ -129,6 +117,17 @@ def _apply_rotary_emb(x, freqs_cis):
     return (x.float() * cos + rotated.float() * sin).to(x.dtype)
 
 
+class _FitResult:
+    """One call's fit: labels, sizes [B,H,K] and stable permutations of Q and K, and the
+    keys the last update fake-quantized (None when not asked for)."""
+
+    __slots__ = ("q_labels", "k_labels", "q_sizes", "k_sizes", "q_idx", "k_idx", "pack")
+
+    def __init__(self, q_labels, k_labels, q_sizes, k_sizes, q_idx, k_idx, pack):
+        self.q_labels, self.k_labels, self.q_sizes, self.k_sizes = q_labels, k_labels, q_sizes, k_sizes
+        self.q_idx, self.k_idx, self.pack = q_idx, k_idx, pack
+
+
 class PecoAttention:
     def __init__(self, layer_idx, config: PecoConfig, context: InferenceContext):
         self.layer_idx = layer_idx
@@ -136,27 +135,40 @@ class PecoAttention:
         self.context = context
         self.q_centroids = None
         self.k_centroids = None
-        self._last_fit = None
-        self._last_pack = None
         # Opt-in extension, not part of the reference's configuration: with Base-Offset on,
         # score video rows against video keys from the codes on the integer MFMA
         # (attention_cuda.base_offset_attention) instead of the fake-quantized rows.
         self.integer_scores = False
+        # Diagnostics: when True, the last call's permutations (q_idx, k_idx) stay in
+        # _last_fit and its fake-quantized keys in _last_pack. Off by default, so a layer
+        # holds nothing between calls but its centroids (as the reference's does).
+        self.record_intermediates = False
+        self._last_fit = None
+        self._last_pack = None
 
     def reset(self):
         self.q_centroids = self.k_centroids = None
         self._last_fit = None
         self._last_pack = None
 
-    def _update_cluster_state(self, query, key, pack_keys=None):
-        """Fit Q/K partitions, reusing this layer's centres after initialization.
+    def _update_cluster_state(self, query, key):
+        """Fit Q/K partitions, reusing this layer's centres after initialization
+        (peco/processor.py:97-113).
 
         query/key are the video parts [B,H,N,D]; returns (q_labels, k_labels, q_sizes, k_sizes)
-        with sizes [B,H,K]. Both fits run in the same launches. With ``pack_keys = (bits,
-        key_full, value_full)`` ([B,H,S,D], key the tensor whose video part is ``key``) the
-        last update also writes K Base-Offset fake-quantized and V, both in the final key
-        cluster order with the text rows after them, into ``self._last_pack``; a fourth entry
-        ``True`` in ``pack_keys`` adds the keys' codes, lows and scales in that order.
+        with sizes [B,H,K]. Both fits run in the same launches.
+        """
+        fit = self._fit_clusters(query, key)
+        return fit.q_labels, fit.k_labels, fit.q_sizes, fit.k_sizes
+
+    def _fit_clusters(self, query, key, pack_keys=None, pack_order="cluster"):
+        """``_update_cluster_state`` returning a _FitResult. With ``pack_keys = (bits, key_full,
+        value_full)`` ([B,H,S,D], key the tensor whose video part is ``key``; value_full None
+        for ``pack_order="original"``) the last update also writes K Base-Offset
+        fake-quantized against its final centres, with the text rows after the video rows:
+        in the final key cluster order together with V, or each row at its own position
+        (``pack_order="original"``, no V). A fourth entry ``True`` adds the keys' codes, lows
+        and scales in the same order. The result's ``pack`` holds these tensors.
         """
         batch, heads, length, dim = query.shape
         initializing = self.q_centroids is None
@@ -173,7 +185,7 @@ class PecoAttention:
         k_init = self._initial_centers(k_flat, self.k_centroids, self.config.num_k_centroids)
         if q_flat.dtype not in (torch.float16, torch.bfloat16, torch.float32) or q_flat.dtype != k_flat.dtype:
             q_flat, k_flat = q_flat.float(), k_flat.float()
-        self._last_pack = None
+        pack = None
         if pack_keys is None:
             problems = [clustering_cuda.KMeansProblem(q_flat, q_init), clustering_cuda.KMeansProblem(k_flat, k_init)]
             outs = clustering_cuda.kmeans_fit(problems, iterations)
@@ -183,20 +195,24 @@ class PecoAttention:
             bits, key_full, value_full = pack_keys[:3]
             with_codes = len(pack_keys) > 3 and pack_keys[3]
             full = key_full.shape[2]
-            if key_full.dtype != k_flat.dtype or not key_full.is_contiguous() or not value_full.is_contiguous():
+            if key_full.dtype != k_flat.dtype or not key_full.is_contiguous() or \
+                    (value_full is not None and not value_full.is_contiguous()):
                 raise ValueError("the packed key and value must be contiguous [B,H,S,D] tensors like key")
             k_rows = key_full.reshape(batch * heads, full, dim)[:, :length]
-            value_flat = value_full.reshape(batch * heads, full, dim)
+            value_flat = None if value_full is None else value_full.reshape(batch * heads, full, dim)
             problems = [clustering_cuda.KMeansProblem(q_flat, q_init), clustering_cuda.KMeansProblem(k_rows, k_init)]
             outs, packed = clustering_cuda.kmeans_fit(problems, iterations,
-                                                      pack=[None, (bits, full, value_flat, with_codes)])
+                                                      pack=[None, (bits, full, value_flat, with_codes)],
+                                                      pack_order=pack_order)
             k_hat, v_perm = packed[1][:2]
-            self._last_pack = (k_hat.view(batch, heads, full, dim), v_perm.view(batch, heads, full, dim),
-                               *packed[1][2:])
+            pack = (k_hat.view(batch, heads, full, dim),
+                    None if v_perm is None else v_perm.view(batch, heads, full, dim), *packed[1][2:])
         (q_labels, q_cent, q_sizes, q_idx, _), (k_labels, k_cent, k_sizes, k_idx, _) = outs
         self.q_centroids, self.k_centroids = q_cent, k_cent
-        self._last_fit = (q_idx, k_idx)
-        return q_labels, k_labels, q_sizes.reshape(batch, heads, -1), k_sizes.reshape(batch, heads, -1)
+        if self.record_intermediates:
+            self._last_fit, self._last_pack = (q_idx, k_idx), pack
+        return _FitResult(q_labels, k_labels, q_sizes.reshape(batch, heads, -1), k_sizes.reshape(batch, heads, -1),
+                          q_idx, k_idx, pack)
 
     @staticmethod
     def _initial_centers(x, cached, clusters):
@@ -231,42 +247,39 @@ class PecoAttention:
         bits = self.config.base_offset_bits
         _validate_bits(bits, allow_bypass=True)
         query, key, value = query.contiguous(), key.contiguous(), value.contiguous()
-        # With Base-Offset on, the last k-means update also writes K fake-quantized and V in
-        # key-cluster order (stages 2-3 of K/V fused into the fit).
         integer = bool(bits) and self.integer_scores
-        q_labels, k_labels, q_sizes, k_sizes = self._update_cluster_state(
-            query[:, :, :video_length], key[:, :, :video_length],
-            pack_keys=(bits, key, value, integer) if bits else None)
-        q_idx, k_idx = self._last_fit
         if integer:
-            # Extension: video x video scores from the Base-Offset codes (see __init__).
+            # Extension: video x video scores from the Base-Offset codes (see __init__). The
+            # last update writes K fake-quantized, V and K's codes in key-cluster order.
+            fit = self._fit_clusters(query[:, :, :video_length], key[:, :, :video_length],
+                                     pack_keys=(bits, key, value, True))
             dynamic_map, ext_q, ext_k = clustering_cuda.select_connections(
                 self.q_centroids.reshape(batch, heads, -1, dim), self.k_centroids.reshape(batch, heads, -1, dim),
-                q_sizes, k_sizes, self.config.top_p,
+                fit.q_sizes, fit.k_sizes, self.config.top_p,
                 math.ceil(self.config.min_kc_ratio * self.config.num_k_centroids), (valid_text, text_length))
-            k_perm, v_perm, k_codes, k_low, k_scale = self._last_pack
-            return base_offset_attention(query, k_perm, v_perm, dynamic_map, ext_q, ext_k, out_index=q_idx,
+            k_perm, v_perm, k_codes, k_low, k_scale = fit.pack
+            return base_offset_attention(query, k_perm, v_perm, dynamic_map, ext_q, ext_k, out_index=fit.q_idx,
                                          q_centroids=self.q_centroids, k_centroids=self.k_centroids,
                                          k_codes=k_codes, k_low=k_low, k_scale=k_scale, bits=bits)
+        # With Base-Offset on, the last k-means update also writes K fake-quantized, each row
+        # at its own position (stage 2 of K fused into the fit).
+        fit = self._fit_clusters(query[:, :, :video_length], key[:, :, :video_length],
+                                 pack_keys=(bits, key, None) if bits else None, pack_order="original")
         # Cluster connectivity from the floating-point centres, extended with the text
         # partition (select_cluster_connections + extend_text_partition), in one launch that
         # also writes each query cluster's kept key segments and the attention's work items.
         work = clustering_cuda.select_work(
             self.q_centroids.reshape(batch, heads, -1, dim), self.k_centroids.reshape(batch, heads, -1, dim),
-            q_sizes, k_sizes, self.config.top_p,
+            fit.q_sizes, fit.k_sizes, self.config.top_p,
             math.ceil(self.config.min_kc_ratio * self.config.num_k_centroids), (valid_text, text_length),
             length, length)
-        if bits == 0:
-            # No fake quantization: attention reads Q/K/V through the sort permutations and
-            # writes the output in original order, so no packed copy is made.
-            return sparse_attention_work(query, key, value, work, out_index=q_idx, out_index_rows=video_length,
-                                         k_index=k_idx)
-        # K (fake-quantized) and V come packed from the fit; Q is read in its original order
-        # through the permutation and fake-quantized as the attention loads it. Video rows
-        # return to their original positions; text rows keep theirs.
-        k_perm, v_perm = self._last_pack[:2]
-        return sparse_attention_work(query, k_perm, v_perm, work, out_index=q_idx, out_index_rows=video_length,
-                                     q_centroids=self.q_centroids, bits=bits)
+        # The attention reads Q/K/V through the sort permutations (stage 3 fused into its
+        # loads) and writes the output in original order, so no packed copy is made. With
+        # Base-Offset on, K comes fake-quantized from the fit and Q is fake-quantized as the
+        # attention loads it.
+        k_in = key if bits == 0 else fit.pack[0]
+        return sparse_attention_work(query, k_in, value, work, out_index=fit.q_idx, out_index_rows=video_length,
+                                     k_index=fit.k_idx, q_centroids=self.q_centroids if bits else None, bits=bits)
 
     @torch.no_grad()
     def __call__(self, attn, hidden_states, encoder_hidden_states=None, attention_mask=None, image_rotary_emb=None):

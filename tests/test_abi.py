@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_library_loads_and_reports_status_strings_without_a_gpu():
     lib = _native.library()
-    assert lib.peco_abi_version() == 4
+    assert lib.peco_abi_version() == 5
     assert b"workspace" in lib.peco_cluster_error_message(20001)
     assert lib.peco_attention_error_string(0)
     # Size queries are host-only arithmetic.

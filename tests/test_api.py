@@ -83,10 +83,9 @@ def test_extend_text_partition_matches_oracle_fixture():
     m = torch.tensor([[[[True, False], [False, True]]]])
     qs = torch.tensor([[[3, 4]]], dtype=torch.int32)
     ks = torch.tensor([[[5, 2]]], dtype=torch.int32)
-    for fn in (processor.extend_text_partition, processor._extend_partition_on_device):
-        em, eq, ek = fn(m, qs, ks, 3, 5)
-        rm, rq, rk = reference_path.extend_text_partition(m, qs, ks, 3, 5)
-        assert torch.equal(em, rm) and torch.equal(eq, rq) and torch.equal(ek, rk)
+    em, eq, ek = processor.extend_text_partition(m, qs, ks, 3, 5)
+    rm, rq, rk = reference_path.extend_text_partition(m, qs, ks, 3, 5)
+    assert torch.equal(em, rm) and torch.equal(eq, rq) and torch.equal(ek, rk)
 
 
 def test_attention_rejects_bad_context():

@@ -1,11 +1,13 @@
 """Base-Offset fake quantization and the cluster gather fused into their neighbours.
 
 With Base-Offset on, the layer has no pack launch:
-- the k-means fit's last update writes K fake-quantized against the final centres and V, both
-  in the final key-cluster order with the text rows after them (peco_kmeans_fit_pack);
+- the k-means fit's last update writes K fake-quantized against the final centres, each row
+  at its own position with the text rows copied (peco_kmeans_fit_pack, hat_order 1; the
+  integer-score extension takes K and V in the final key-cluster order instead, hat_order 0);
 - the attention reads Q in its original order through the permutation and fake-quantizes it
-  as it loads the rows (peco_sparse_attention_work with q_centroids).
-Both must equal the standalone pack launch (itself checked against the oracle's
+  as it loads the rows, and K/V through the key permutation (peco_sparse_attention_work with
+  q_centroids and k_index).
+All must equal the standalone pack launch (itself checked against the oracle's
 fake_quantize + gather + concat in test_gpu_stages.py) bit for bit, and the attention over
 them must equal the attention over packed inputs bit for bit.
 """
@@ -93,5 +95,64 @@ def test_attention_quantizes_queries_at_load(announce, dtype, d, bits):
     ref = attention_cuda.sparse_attention_work(q_hat, k_hat, v_out, work, out_index=q_idx, out_index_rows=n)
     out = attention_cuda.sparse_attention_work(q, k_hat, v_out, work, out_index=q_idx, out_index_rows=n,
                                                q_centroids=q_cent, bits=bits)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("dtype,d,h,n,text,kq,kk,bits,iters", [
+    (torch.bfloat16, 128, 3, 2000, 40, 12, 30, 4, 3),
+    (torch.bfloat16, 128, 2, 9000, 32, 16, 40, 4, 2),
+    (torch.float16, 64, 2, 3000, 16, 10, 20, 8, 2),
+    (torch.bfloat16, 128, 2, 1500, 0, 8, 24, 4, 2),
+])
+def test_fit_packs_keys_in_original_order(announce, dtype, d, h, n, text, kq, kk, bits, iters):
+    """pack_order="original": row t < N of the packed keys is key row t fake-quantized against
+    its final centre (the cluster-order pack scattered back through the permutation), rows
+    past N are the text rows unchanged, and the fit itself is unchanged."""
+    q, k, v, q_init, k_init = _fit_inputs(d + n + bits + 1, h, n, text, d, dtype, kq, kk)
+    length = n + text
+    announce(f"{dtype} D={d} H={h} N={n} text={text} KQ={kq} KK={kk} bits={bits} iters={iters}")
+    problems = [clustering_cuda.KMeansProblem(q[0, :, :n], q_init), clustering_cuda.KMeansProblem(k[0, :, :n], k_init)]
+    plain = clustering_cuda.kmeans_fit(problems, iters)
+    outs, packed = clustering_cuda.kmeans_fit(problems, iters, pack=[None, (bits, length, None)],
+                                              pack_order="original")
+    for a, b in zip(plain, outs):
+        for x, y in zip(a, b):
+            assert torch.equal(x, y)
+    k_labels, k_cent, _, k_idx, _ = outs[1]
+    k_hat, v_out = packed[1]
+    assert v_out is None
+    (ref_k,) = clustering_cuda.pack_clustered([k], [k_idx], [k_labels], [k_cent], [bits], n)
+    expect = ref_k[0].clone()
+    expect[:, :n] = torch.empty_like(expect[:, :n]).scatter_(
+        1, k_idx.long()[..., None].expand(-1, -1, d), ref_k[0, :, :n])
+    torch.cuda.synchronize()
+    assert _bits_equal(k_hat.cpu(), expect.cpu())
+    assert _bits_equal(k_hat[:, n:].cpu(), k[0, :, n:].cpu())
+    with pytest.raises(ValueError, match="pack_order"):
+        clustering_cuda.kmeans_fit(problems, iters, pack=[None, (bits, length, v[0])], pack_order="original")
+
+
+@pytest.mark.parametrize("dtype,d,bits", [(torch.bfloat16, 128, 4), (torch.float16, 64, 8), (torch.bfloat16, 64, 4)])
+def test_attention_quantizes_queries_with_indexed_keys(announce, dtype, d, bits):
+    """The layer's Base-Offset attention (Q quantized at load, K fake-quantized in original
+    order, V the input itself, both read through the key permutation) equals the attention
+    over the cluster-order pack bit for bit."""
+    h, n, text, valid, kq, kk = 4, 3000, 48, 37, 16, 48
+    q, k, v, q_init, k_init = _fit_inputs(d * 3 + bits + 1, h, n, text, d, dtype, kq, kk)
+    length = n + text
+    announce(f"{dtype} D={d} bits={bits}")
+    problems = [clustering_cuda.KMeansProblem(q[0, :, :n], q_init), clustering_cuda.KMeansProblem(k[0, :, :n], k_init)]
+    outs, packed = clustering_cuda.kmeans_fit(problems, 2, pack=[None, (bits, length, v[0])])
+    (q_labels, q_cent, q_sizes, q_idx, _), (_, k_cent, k_sizes, k_idx, _) = outs
+    k_perm, v_perm = (t[None] for t in packed[1])
+    _, packed_o = clustering_cuda.kmeans_fit(problems, 2, pack=[None, (bits, length, None)], pack_order="original")
+    k_hat = packed_o[1][0][None]
+    work = clustering_cuda.select_work(q_cent[None], k_cent[None], q_sizes[None], k_sizes[None], 0.7, 4,
+                                       (valid, text), length, length)
+    ref = attention_cuda.sparse_attention_work(q, k_perm, v_perm, work, out_index=q_idx, out_index_rows=n,
+                                               q_centroids=q_cent, bits=bits)
+    out = attention_cuda.sparse_attention_work(q, k_hat, v, work, out_index=q_idx, out_index_rows=n,
+                                               k_index=k_idx, q_centroids=q_cent, bits=bits)
     torch.cuda.synchronize()
     assert torch.equal(out, ref)

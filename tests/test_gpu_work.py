@@ -207,6 +207,31 @@ def test_work_buffer_serves_consecutive_calls(announce):
         _check_work(work, emap, eqs, eks, sq, sk)
 
 
+def test_overwritten_work_list_is_rejected(announce):
+    """A later select_work of the same shape on the same stream reuses the buffer: the
+    earlier SelectionWork reports itself invalid and the attention refuses it, while the
+    latest one (and one of another shape, with its own buffer) still runs."""
+    h, cq, ck, video, text, valid, d = 2, 16, 48, 2000, 24, 24, 64
+    q, k, v, qs, ks, qidx, kidx, qc, kc = _clustered_inputs(11, h, cq, ck, video, text, d, torch.bfloat16)
+    length = video + text
+    announce(f"H={h} N={video} CQ={cq} CK={ck}")
+    q, k, v, qidx, kidx = (t.to(DEV) for t in (q, k, v, qidx, kidx))
+    args = (qc.to(DEV), kc.to(DEV), qs.to(DEV), ks.to(DEV))
+    first = clustering_cuda.select_work(*args, 0.6, 4, (valid, text), length, length)
+    assert first.valid()
+    second = clustering_cuda.select_work(*args, 0.8, 4, (valid, text), length, length)
+    assert not first.valid() and second.valid()
+    kw = dict(out_index=qidx, out_index_rows=video, k_index=kidx)
+    with pytest.raises(RuntimeError, match="overwritten"):
+        attention_cuda.sparse_attention_work(q, k, v, first, **kw)
+    out = attention_cuda.sparse_attention_work(q, k, v, second, **kw)
+    emap, eqs, eks, kept = clustering_cuda.select_connections(*args, 0.8, 4, text=(valid, text), with_kept=True)
+    ref = attention_cuda.sparse_attention_indexed(q, k, v, emap, eqs, eks, qidx, kidx, video, validate_sizes=False,
+                                                  kept_keys=kept)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+
+
 @pytest.mark.parametrize("indexed", [True, False])
 def test_persistent_grid_equals_map_attention(announce, indexed):
     """A launch with at least 8 item slots per resident workgroup (16 heads x 32896 rows, 130 x
