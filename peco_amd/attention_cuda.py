@@ -241,7 +241,7 @@ def sparse_attention_work(
         if not _device_is_gfx950(q.device):
             raise RuntimeError("This HIP build requires an MI355X-class gfx950 GPU")
         library = _native.library()
-        stream = _native.current_stream(q.device, q, k, v, work.buffer, output, out_index, k_index, q_centroids)
+        stream = _native.current_stream(q.device, q, k, v, work.buffer, out_index, k_index, q_centroids)
         events = launch_events
         if events is not None:
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

@@ -176,7 +176,9 @@ def kmeans_fit(problems, iterations, pack=None, pack_order="cluster"):
         ws_bytes += library.peco_kmeans_workspace_size(p.batch, p.tokens, p.clusters, dims)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     strides = (ctypes.c_int64 * len(problems))(*[p.x.stride(0) for p in problems])
-    tensors = [p.x for p in problems] + [p.init for p in problems] + [t for o in outs for t in o] + [ws]
+    # Only the caller's tensors need recording: the outputs and the workspace are allocated
+    # here, on the stream the launches run on.
+    tensors = [p.x for p in problems] + [p.init for p in problems]
     common = (
         len(problems),
         _native.ptr_array([p.x for p in problems]), ctypes.cast(strides, ctypes.c_void_p),
@@ -222,7 +224,7 @@ def kmeans_fit(problems, iterations, pack=None, pack_order="cluster"):
                          torch.empty((p.batch, p.tokens), dtype=torch.float32, device=dev),
                          torch.empty((p.batch, p.tokens), dtype=torch.float32, device=dev)) if want_codes else None)
     codes, lows, scales = ([None if q is None else q[i] for q in payloads] for i in range(3))
-    extra = [t for t in hats + withs_in + withs_out + codes + lows + scales if t is not None]
+    extra = [t for t in withs_in if t is not None]
     with torch.cuda.device(dev):
         status = library.peco_kmeans_fit_pack(
             *common, _native.ptr_array(hats), _native.int_array(bits), _native.ptr_array(withs_in),

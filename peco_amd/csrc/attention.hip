@@ -261,23 +261,6 @@ template <int D> struct Tiles {
 };
 
 
-// One 16-byte-per-lane direct load from global memory into the LDS span starting at byte
-// address lds (M0). Written as inline assembly so that the compiler's wait-count pass does not
-// see an LDS write in flight: it cannot tell the buffer being filled from the one being read
-// by the transpose reads and would otherwise wait for the whole prefetch in the middle of
-// every tile. The caller waits for vmcnt(0) before the barrier that publishes the tile.
-__device__ __forceinline__ void dma16(const uint16_t* src, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
-}
-
-// The same with 4 bytes per lane: lane i writes lds + 4i.
-__device__ __forceinline__ void dma4(const void* src, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p)));
-}
 
 // Issue the direct-to-LDS loads of one K and one V tile (no wait), or the share of a wave
 // that is one of NL loaders (rank `first`): the tile's 4*kLoads spans of 64 lanes x 16 bytes
@@ -1314,21 +1297,6 @@ int attention_head_band(int bh, int sk, int d) {
 // Launch of the attention kernel over a built work list (map + kprefix, or segs).
 // q_centroids (nullable, with out_index) selects the kQuantQ input mode, or kIndexedQuantQ
 // with k_index.
-// Compute units of the current device (cached per device).
-int device_compute_units() {
-    static std::mutex m;
-    static int cus[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    std::lock_guard<std::mutex> lock(m);
-    if (!cus[dev]) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 256;
-        cus[dev] = n;
-    }
-    return cus[dev];
-}
-
 // queues (nullable): the work list's item queue counters. Given, and with at least
 // kPersistItems item slots per resident workgroup, the grid is the persistent one of
 // sparse_attention_kernel (two resident workgroups per CU take items from the queues): 544p

@@ -9,6 +9,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #define PECO_API extern "C" __attribute__((visibility("default")))
 
 namespace peco {
@@ -94,5 +96,42 @@ template <typename T> __device__ __forceinline__ T wave_shfl_xor(T v, int mask) 
 }
 
 __host__ __device__ __forceinline__ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Compute units of the current device (cached per device; 256 if the query fails).
+inline int device_compute_units() {
+    static std::mutex m;
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    std::lock_guard<std::mutex> lock(m);
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+// One 16-byte-per-lane direct load from global memory into the LDS span starting at byte
+// address lds (M0). Written as inline assembly so that the compiler's wait-count pass does not
+// see an LDS write in flight: it cannot tell the buffer being filled from the one being read
+// by the fragment reads and would otherwise wait for the whole prefetch in the middle of
+// every tile. The caller waits for vmcnt(0) before the barrier that publishes the tile.
+__device__ __forceinline__ void dma16(const uint16_t* src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+
+// The same with 4 bytes per lane: lane i writes lds + 4i.
+__device__ __forceinline__ void dma4(const void* src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p)));
+}
+
+// XCDs of an MI355X: workgroup i of a launch is dispatched to XCD i % kXcdCount, each with
+// its own L2.
+constexpr int kXcdCount = 8;
 
 }  // namespace peco
