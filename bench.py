@@ -86,9 +86,8 @@ def stage_breakdown(layer, wl, q, k, v, q_init, k_init, reps):
 
     The stages follow ``PecoAttention.attention``: the selection launch also writes the
     attention's work list (kept-segment lists and ordered items). The attention reads Q/K/V
-    through the sort permutations; with Base-Offset on, the fit's last update also writes K
-    fake-quantized in original order and the attention fake-quantizes Q as it loads it, so
-    there is no pack stage. The repetitions are queued back to back, as the layer steps are,
+    through the sort permutations; with Base-Offset on, the fit ends with a launch that writes
+    Q and K fake-quantized in original order, counted in the k-means stage. The repetitions are queued back to back, as the layer steps are,
     so the host's launch work overlaps the device's; the first repetition, which starts on
     an idle device, is not counted.
     """
@@ -105,7 +104,7 @@ def stage_breakdown(layer, wl, q, k, v, q_init, k_init, reps):
         ev[0].record()
         layer.q_centroids, layer.k_centroids = q_init, k_init
         fit = layer._fit_clusters(q[:, :, :n], k[:, :, :n], pack_keys=(s.bits, k, None) if s.bits else None,
-                                  pack_order="original")
+                                  pack_order="original", query_full=q if s.bits else None)
         qs, ks, q_idx, k_idx = fit.q_sizes, fit.k_sizes, fit.q_idx, fit.k_idx
         ev[1].record()
         work = clustering_cuda.select_work(
@@ -115,7 +114,7 @@ def stage_breakdown(layer, wl, q, k, v, q_init, k_init, reps):
         if s.bits == 0:
             attn_args = (q, k, v, work, q_idx, k_idx, n, None, 0)
         else:
-            attn_args = (q, fit.pack[0], v, work, q_idx, k_idx, n, layer.q_centroids, s.bits)
+            attn_args = (fit.q_hat, fit.pack[0], v, work, q_idx, k_idx, n, None, 0)
         run_attention(attn_args)
         ev[3].record()
         events.append(ev)

@@ -13,6 +13,8 @@
 // a zero bound cannot change a code or a reconstruction).
 #pragma once
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace peco {
@@ -38,17 +40,23 @@ __device__ __forceinline__ BaseOffsetRow base_offset_row(float low, float high, 
     return p;
 }
 
+// Reconstruction from a rounded quotient q: the code clamped to [0, levels] (v_med3, equal to
+// the two-sided clamp for every finite q) and C + (low + scale * code).
+__device__ __forceinline__ float base_offset_rebuild(float q, float c, const BaseOffsetRow& p, uint32_t& code) {
+    q = __builtin_amdgcn_fmed3f(q, 0.0f, p.levels);
+    code = static_cast<uint32_t>(q);
+    const float step = p.scale * q;
+    const float resid = p.low + step;
+    return c + resid;
+}
+
 // Code and reconstruction of one residual r = x - c.
 __device__ __forceinline__ float base_offset_value(float r, float c, const BaseOffsetRow& p, uint32_t& code) {
     const float shifted = r - p.low;
     const float qa = shifted * p.inv;
     float q = __builtin_rintf(qa);
     if (fabsf(qa - q) >= 0.5f - p.tol) q = __builtin_rintf(shifted / p.scale);
-    q = q < 0.0f ? 0.0f : (q > p.levels ? p.levels : q);
-    code = static_cast<uint32_t>(q);
-    const float step = p.scale * q;
-    const float resid = p.low + step;
-    return c + resid;
+    return base_offset_rebuild(q, c, p, code);
 }
 
 // Eight consecutive elements of a row: loads as fp32, stores with RNE, bit copies.
@@ -99,6 +107,22 @@ __device__ __forceinline__ void load_centroid8(const float* c, float (&v)[8]) {
     for (int i = 0; i < 4; ++i) { v[i] = a[i]; v[4 + i] = b[i]; }
 }
 
+// Minimum and maximum over an aligned group of G lanes (8 or 16, inside one 16-lane DPP row):
+// DPP moves (swaps within quads, then the half-row and row mirrors) instead of LDS permutes.
+template <int G>
+__device__ __forceinline__ void group_min_max(float& lo, float& hi) {
+    static_assert(G == 8 || G == 16, "lane groups of 8 or 16");
+    auto step = [&](auto ctrl) __attribute__((always_inline)) {
+        constexpr int C = decltype(ctrl)::value;
+        lo = fminf(lo, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(lo), C, 0xf, 0xf, false)));
+        hi = fmaxf(hi, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(hi), C, 0xf, 0xf, false)));
+    };
+    step(std::integral_constant<int, 0xb1>{});   // quad_perm [1, 0, 3, 2]: lane ^ 1
+    step(std::integral_constant<int, 0x4e>{});   // quad_perm [2, 3, 0, 1]: lane ^ 2
+    step(std::integral_constant<int, 0x141>{});  // row_half_mirror: quads 0-1 and 2-3 meet
+    if constexpr (G == 16) step(std::integral_constant<int, 0x140>{});  // row_mirror: the two halves meet
+}
+
 // Quantize 8 residual channels of one token held by this lane; the lane group of G lanes
 // together holds the whole token. Returns codes, writes xhat, low and scale.
 template <int G>
@@ -113,17 +137,31 @@ __device__ __forceinline__ void base_offset_lane(const float (&x)[8], const floa
         lo = fminf(lo, r[i]);
         hi = fmaxf(hi, r[i]);
     }
-#pragma unroll
-    for (int m = 1; m < G; m <<= 1) {
-        lo = fminf(lo, __shfl_xor(lo, m, G));
-        hi = fmaxf(hi, __shfl_xor(hi, m, G));
-    }
+    group_min_max<G>(lo, hi);
     const BaseOffsetRow p = base_offset_row(lo, hi, levels);
+    // base_offset_value for the 8 channels, with one branch for the rare near-half quotients
+    // of the lane instead of one per channel.
+    float shifted[8], q[8];
+    float near = 0.0f;  // largest |qa - rint(qa)| of the lane
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        uint32_t q;
-        xhat[i] = base_offset_value(r[i], c[i], p, q);
-        code[i] = static_cast<uint8_t>(q);
+        shifted[i] = r[i] - p.low;
+        const float qa = shifted[i] * p.inv;
+        q[i] = __builtin_rintf(qa);
+        near = __builtin_fmaxf(near, fabsf(qa - q[i]));
+    }
+    if (near >= 0.5f - p.tol) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float qa = shifted[i] * p.inv;
+            if (fabsf(qa - q[i]) >= 0.5f - p.tol) q[i] = __builtin_rintf(shifted[i] / p.scale);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        uint32_t k;
+        xhat[i] = base_offset_rebuild(q[i], c[i], p, k);
+        code[i] = static_cast<uint8_t>(k);
     }
     low_out = p.low;
     scale_out = p.scale;

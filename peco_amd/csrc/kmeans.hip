@@ -64,6 +64,8 @@ struct KmProblem {
     int upd_begin;          // first linear km_update_kernel workgroup of this problem
     int upd_blocks;
     int upd_shared;         // 1: one workgroup per cluster, 0: one wavefront per cluster
+    int pack_begin;         // first linear km_pack_rows_kernel workgroup (hat_order 1 only)
+    int pack_blocks;        // batch * ceil(length / rows per packing workgroup)
     // Packing by the last update (nullable hat): rows [0, tokens) of hat [batch, length, D]
     // receive x's rows in cluster order, Base-Offset fake-quantized (hat_bits) against the
     // final centres, and rows [tokens, length) x's own rows past `tokens` (text, in the same
@@ -71,7 +73,8 @@ struct KmProblem {
     // without quantization. codes/low/scale (nullable together, [batch, tokens, D] uint8 and
     // [batch, tokens] fp32) receive the packed rows' Base-Offset payload in the same order.
     // hat_order 1 writes every row at its own token position instead (original order; no
-    // with_in/with_out then), so hat is x with its video rows fake-quantized.
+    // with_in/with_out then), so hat is x with its video rows fake-quantized: a token-parallel
+    // launch after the last update (km_pack_rows_kernel) rather than the update's own pass.
     void* hat;
     const void* with_in;
     void* with_out;
@@ -96,6 +99,7 @@ struct KmArgs {
     int total_scan_blocks;
     int total_upd_blocks;
     int text_blocks;  // packing launch only: workgroups after the update's that copy text rows
+    int total_pack_blocks;  // km_pack_rows_kernel grid (problems packed in original order)
     float kappa;      // bound coefficient: |screened - canonical| <= kappa*|x||c| + rounding terms
     float gamma_acc;  // gamma of the MFMA accumulation length (applied to the norm term)
 };
@@ -819,11 +823,11 @@ __device__ __forceinline__ int km_update_problem(const KmArgs& a, int block) {
     return p;
 }
 
-// Packing pass of the last update: the members of one cluster, in sorted order m (their
-// packed row, or with P.hat_order their own token row), 16 lanes per row (8 channels each; 8
-// lanes at D = 64). The members go 64 at a time (`first`, `stride`: this wavefront's first
-// member and step); one index load per lane, then the rows of 8 passes (32 or 64 rows) are
-// requested together before any is used.
+// Packing pass of the last update (cluster order): the members of one cluster, in sorted
+// order m (their packed row), 16 lanes per row (8 channels each; 8 lanes at D = 64). The
+// members go 64 at a time (`first`, `stride`: this wavefront's first member and step); one
+// index load per lane, then the rows of 8 passes (32 or 64 rows) are requested together
+// before any is used.
 template <int DT> struct Raw8 {
     u32x4 v[DT == kF32 ? 2 : 1];
     __device__ __forceinline__ void load(const void* base, int64_t e) {
@@ -836,10 +840,39 @@ template <int DT> struct Raw8 {
 #pragma unroll
         for (int i = 0; i < (DT == kF32 ? 2 : 1); ++i) p[i] = v[i];
     }
+    // The 8 elements as fp32 (the conversion of Row8<DT>::load).
+    __device__ __forceinline__ void to_f32(float (&f)[8]) const {
+        if constexpr (DT == kF32) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                f[i] = __uint_as_float(v[0][i]);
+                f[4 + i] = __uint_as_float(v[1][i]);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                f[2 * i] = half_to_f32<DT>(static_cast<uint16_t>(v[0][i] & 0xffffu));
+                f[2 * i + 1] = half_to_f32<DT>(static_cast<uint16_t>(v[0][i] >> 16));
+            }
+        }
+    }
 };
 
-// kOriginal: rows go to their own token positions (P.hat_order 1), with no companion tensor.
-template <int DT, int D, bool kOriginal>
+// Base-Offset payload of 8 channels of payload row `row` (codes; the row's low and scale
+// from the lane holding its first channels).
+__device__ __forceinline__ void store_payload(const KmProblem& P, int64_t row, int sub, int D, const uint8_t (&q)[8],
+                                              float lo, float sc) {
+    u32x2 packed;
+    packed[0] = q[0] | (q[1] << 8) | (q[2] << 16) | (static_cast<uint32_t>(q[3]) << 24);
+    packed[1] = q[4] | (q[5] << 8) | (q[6] << 16) | (static_cast<uint32_t>(q[7]) << 24);
+    *reinterpret_cast<u32x2*>(P.codes + row * D + sub * 8) = packed;
+    if (sub == 0) {
+        P.low[row] = lo;
+        P.scale[row] = sc;
+    }
+}
+
+template <int DT, int D>
 __device__ __forceinline__ void pack_members(const KmProblem& P, int b, int begin, int end, const float* centre,
                                              int first, int stride) {
     constexpr int G = D / 8;       // lanes per row
@@ -850,7 +883,7 @@ __device__ __forceinline__ void pack_members(const KmProblem& P, int b, int begi
     const int sub = lane % G, rsub = lane / G;
     const int32_t* idx = P.indices + static_cast<int64_t>(b) * P.tokens;
     const float levels = static_cast<float>((1 << P.hat_bits) - 1);
-    const bool with = !kOriginal && P.with_out != nullptr;
+    const bool with = P.with_out != nullptr;
     float c[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) c[i] = centre[sub * 8 + i];
@@ -859,17 +892,13 @@ __device__ __forceinline__ void pack_members(const KmProblem& P, int b, int begi
         const int mine = idx[m0 + min(lane, cnt - 1)];
         for (int u0 = 0; u0 < PASSES && u0 * R < cnt; u0 += U) {
             float xv[U][8];
-            Raw8<DT> wv[kOriginal ? 1 : U];
-            int toks[kOriginal ? U : 1];
+            Raw8<DT> wv[U];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int r = min((u0 + u) * R + rsub, cnt - 1);  // clamped: every load is unconditional
                 const int tok = __shfl(mine, r, kWave);
-                if constexpr (kOriginal) toks[u] = tok;
                 Row8<DT>::load(P.x, b * P.x_stride + static_cast<int64_t>(tok) * D + sub * 8, xv[u]);
-                if constexpr (!kOriginal) {
-                    if (with) wv[u].load(P.with_in, (static_cast<int64_t>(b) * P.length + tok) * D + sub * 8);
-                }
+                if (with) wv[u].load(P.with_in, (static_cast<int64_t>(b) * P.length + tok) * D + sub * 8);
             }
 #pragma unroll
             for (int u = 0; u < U; ++u) {
@@ -878,30 +907,19 @@ __device__ __forceinline__ void pack_members(const KmProblem& P, int b, int begi
                 uint8_t q[8];
                 base_offset_lane<G>(xv[u], c, levels, out, q, lo, sc);
                 if (r < cnt) {
-                    const int pos = kOriginal ? toks[kOriginal ? u : 0] : m0 + r;
+                    const int pos = m0 + r;
                     const int64_t dst = (static_cast<int64_t>(b) * P.length + pos) * D + sub * 8;
                     Row8<DT>::store(P.hat, dst, out);
-                    if constexpr (!kOriginal) {
-                        if (with) wv[u].store(P.with_out, dst);
-                    }
-                    if (P.codes) {
-                        const int64_t row = static_cast<int64_t>(b) * P.tokens + pos;
-                        u32x2 packed;
-                        packed[0] = q[0] | (q[1] << 8) | (q[2] << 16) | (static_cast<uint32_t>(q[3]) << 24);
-                        packed[1] = q[4] | (q[5] << 8) | (q[6] << 16) | (static_cast<uint32_t>(q[7]) << 24);
-                        *reinterpret_cast<u32x2*>(P.codes + row * D + sub * 8) = packed;
-                        if (sub == 0) {
-                            P.low[row] = lo;
-                            P.scale[row] = sc;
-                        }
-                    }
+                    if (with) wv[u].store(P.with_out, dst);
+                    if (P.codes) store_payload(P, static_cast<int64_t>(b) * P.tokens + pos, sub, D, q, lo, sc);
                 }
             }
         }
     }
 }
 
-// Text rows [tokens, length) of every packed problem, copied into hat and with_out.
+// Text rows [tokens, length) of every problem packed in cluster order, copied into hat and
+// with_out.
 template <int DT, int D>
 __device__ __forceinline__ void pack_text_rows(const KmArgs& a, int block) {
     constexpr int G = D / 8;
@@ -909,7 +927,7 @@ __device__ __forceinline__ void pack_text_rows(const KmArgs& a, int block) {
     const int nthreads = a.text_blocks * kUpdateWaves * kWave;
     for (int p = 0; p < a.num; ++p) {
         const KmProblem& P = a.p[p];
-        if (!P.hat) continue;
+        if (!P.hat || P.hat_order) continue;
         const int text = P.length - P.tokens;
         const int64_t rows = static_cast<int64_t>(P.batch) * text;
         for (int64_t r = (static_cast<int64_t>(block) * kUpdateWaves * kWave + threadIdx.x) / G; r < rows;
@@ -923,8 +941,8 @@ __device__ __forceinline__ void pack_text_rows(const KmArgs& a, int block) {
     }
 }
 
-// kPack: 0 plain update; 1 the last update of a packing fit in cluster order, 2 in original
-// order (P.hat_order 1; every packing problem of the launch has the same order).
+// kPack: 0 plain update; 1 the last update of a fit that packs some problem in cluster order
+// (those problems' members are packed by the update itself).
 template <int DT, int D, int kPack = 0>
 __global__ __launch_bounds__(kUpdateWaves * kWave) void km_update_kernel(KmArgs a, KmIter it) {
     constexpr int PER = D / kWave;  // channels per lane (1 or 2)
@@ -986,10 +1004,10 @@ __global__ __launch_bounds__(kUpdateWaves * kWave) void km_update_kernel(KmArgs 
         }
         if (wave != 0) {
             if constexpr (kPack) {
-                if (P.hat) {
+                if (P.hat && !P.hat_order) {
                     // The other wavefronts pack with wave 0 once it has left the centre in row[0].
                     __syncthreads();
-                    pack_members<DT, D, kPack == 2>(P, b, begin, end, row[0], kWave * wave, kWave * kUpdateWaves);
+                    pack_members<DT, D>(P, b, begin, end, row[0], kWave * wave, kWave * kUpdateWaves);
                 }
             }
             return;
@@ -1018,13 +1036,82 @@ __global__ __launch_bounds__(kUpdateWaves * kWave) void km_update_kernel(KmArgs 
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     if (lane == 0) P.norms[cl] = canonical_norm_lds(row[wave], D);
     if constexpr (kPack) {
-        if (P.hat) {
+        if (P.hat && !P.hat_order) {
             if (shared) {
                 __syncthreads();  // row[0] (this wavefront's centre) is published to the others
-                pack_members<DT, D, kPack == 2>(P, b, begin, end, row[0], 0, kWave * kUpdateWaves);
+                pack_members<DT, D>(P, b, begin, end, row[0], 0, kWave * kUpdateWaves);
             } else {
-                pack_members<DT, D, kPack == 2>(P, b, begin, end, row[wave], 0, kWave);
+                pack_members<DT, D>(P, b, begin, end, row[wave], 0, kWave);
             }
+        }
+    }
+}
+
+// Packing in original order (P.hat_order 1), after the last update: row t of hat [b, length, D]
+// is x's row t, Base-Offset fake-quantized (hat_bits) against the final centre of its label for
+// t < tokens and copied bit for bit past it (text). G = D / 8 lanes per row (8 channels each),
+// kPackRowPasses passes of 256 / G rows per workgroup over one batch entry; the labels and rows
+// of every pass are requested first, then the centres the labels select.
+constexpr int kPackRowPasses = 4;
+
+template <int D> constexpr int pack_rows_per_block() { return kPackRowPasses * 256 / (D / 8); }
+
+template <int DT, int D>
+__global__ __launch_bounds__(256) void km_pack_rows_kernel(KmArgs a, KmIter it) {
+    constexpr int G = D / 8;
+    constexpr int R = 256 / G;
+    constexpr int U = kPackRowPasses;
+    int p = 0;
+    while (p + 1 < a.num && !(static_cast<int>(blockIdx.x) >= a.p[p].pack_begin &&
+                              static_cast<int>(blockIdx.x) < a.p[p].pack_begin + a.p[p].pack_blocks))
+        ++p;
+    const KmProblem& P = a.p[p];
+    const int per_batch = static_cast<int>(ceil_div(P.length, R * U));
+    const int local = static_cast<int>(blockIdx.x) - P.pack_begin;
+    const int b = local / per_batch;
+    const int t0 = (local % per_batch) * R * U + static_cast<int>(threadIdx.x) / G;
+    const int sub = threadIdx.x % G;
+    const int K = P.clusters;
+    const float levels = static_cast<float>((1 << P.hat_bits) - 1);
+    const float* cent = it.dst[p] + static_cast<int64_t>(b) * K * D + sub * 8;
+    // Labels first, then the rows: the centre loads wait for the labels only, so their
+    // latency overlaps the rows'.
+    Raw8<DT> raw[U];
+    int label[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+        label[u] = P.labels[static_cast<int64_t>(b) * P.tokens + min(t0 + u * R, P.tokens - 1)];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int t = min(t0 + u * R, P.length - 1);  // clamped: every load is unconditional
+        raw[u].load(P.x, static_cast<int64_t>(b) * P.x_stride + static_cast<int64_t>(t) * D + sub * 8);
+    }
+    float c[U][8];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int j = min(static_cast<unsigned>(label[u]), static_cast<unsigned>(K - 1));
+        const f32x4* src = reinterpret_cast<const f32x4*>(cent + static_cast<int64_t>(j) * D);
+        const f32x4 lo4 = src[0], hi4 = src[1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            c[u][i] = lo4[i];
+            c[u][4 + i] = hi4[i];
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int t = t0 + u * R;
+        float xv[8], out[8], lo, sc;
+        uint8_t q[8];
+        raw[u].to_f32(xv);
+        base_offset_lane<G>(xv, c[u], levels, out, q, lo, sc);
+        if (t >= P.length) continue;
+        const int64_t dst = (static_cast<int64_t>(b) * P.length + t) * D + sub * 8;
+        if (t < P.tokens) {
+            Row8<DT>::store(P.hat, dst, out);
+            if (P.codes) store_payload(P, static_cast<int64_t>(b) * P.tokens + t, sub, D, q, lo, sc);
+        } else {
+            raw[u].store(P.hat, dst);
         }
     }
 }
@@ -1145,17 +1232,19 @@ hipError_t run_fit(KmArgs& a, const KmIter* iters, int iterations, SortArgs sa, 
         }
         hipError_t e = launch_cluster_sort(sa, s, false);
         if (e != hipSuccess) return e;
-        bool original = false;
-        for (int q = 0; q < a.num; ++q) original = original || (a.p[q].hat && a.p[q].hat_order);
-        if (i + 1 == iterations && a.text_blocks > 0 && original)
-            hipLaunchKernelGGL((km_update_kernel<DT, D, 2>), dim3(a.total_upd_blocks + a.text_blocks),
-                               dim3(kUpdateWaves * kWave), 0, s, a, iters[i]);
-        else if (i + 1 == iterations && a.text_blocks > 0)
+        bool cluster_order = false, original = false;
+        for (int q = 0; q < a.num; ++q) {
+            cluster_order = cluster_order || (a.p[q].hat && !a.p[q].hat_order);
+            original = original || (a.p[q].hat && a.p[q].hat_order);
+        }
+        if (i + 1 == iterations && cluster_order)
             hipLaunchKernelGGL((km_update_kernel<DT, D, 1>), dim3(a.total_upd_blocks + a.text_blocks),
                                dim3(kUpdateWaves * kWave), 0, s, a, iters[i]);
         else
             hipLaunchKernelGGL((km_update_kernel<DT, D>), dim3(a.total_upd_blocks), dim3(kUpdateWaves * kWave), 0, s,
                                a, iters[i]);
+        if (i + 1 == iterations && original)
+            hipLaunchKernelGGL((km_pack_rows_kernel<DT, D>), dim3(a.total_pack_blocks), dim3(256), 0, s, a, iters[i]);
     }
     return hipGetLastError();
 }
@@ -1273,7 +1362,12 @@ hipError_t km_fit(const KmFitDesc* descs, int num, int dims, int dtype, int iter
         P.hat_bits = d.hat_bits;
         P.length = d.length;
         P.hat_order = d.hat_order;
-        if (d.hat) {
+        if (d.hat && d.hat_order) {
+            P.pack_blocks = d.batch * static_cast<int>(ceil_div(d.length, dims == 128 ? pack_rows_per_block<128>()
+                                                                                     : pack_rows_per_block<64>()));
+            P.pack_begin = a.total_pack_blocks;
+            a.total_pack_blocks += P.pack_blocks;
+        } else if (d.hat) {
             // Text copies: one 16-byte chunk per thread and row, at most 64 workgroups.
             const int64_t chunks = static_cast<int64_t>(d.batch) * std::max(d.length - d.tokens, 0) * (dims / 8);
             a.text_blocks = std::max(a.text_blocks, static_cast<int>(std::min<int64_t>(

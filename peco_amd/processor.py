@@ -2,15 +2,16 @@
 
 The sparse path of ``PecoAttention.attention`` runs as three groups of device launches:
   1. fused Q+K k-means (clustering_cuda.kmeans_fit): labels, centres, sizes and the
-     stable cluster permutation of both tensors. With Base-Offset on, the last update also
-     writes K fake-quantized against its final centre, row for row in original order;
+     stable cluster permutation of both tensors. With Base-Offset on, a token-parallel
+     launch after the last update writes Q and K fake-quantized against their final
+     centres, row for row in original order (text rows copied);
   2. one selection launch (clustering_cuda.select_work): cluster-pair selection with the
      text partition appended, each query cluster's kept key segments and the attention's
      cost-ordered work items;
-  3. the MFMA sparse attention, which reads Q, K (or its fake-quantized copy) and V through
-     the sort permutations, fake-quantizes Q as it loads it when Base-Offset is on, and
-     writes every video row straight back to its original sequence position.
-No packed Q/K/V copies and no concatenations are made.
+  3. the MFMA sparse attention, which reads Q, K (or their fake-quantized copies) and V
+     through the sort permutations and writes every video row straight back to its original
+     sequence position.
+No cluster-order Q/K/V copies and no concatenations are made.
 """
 from __future__ import annotations
 
@@ -121,11 +122,11 @@ class _FitResult:
     """One call's fit: labels, sizes [B,H,K] and stable permutations of Q and K, and the
     keys the last update fake-quantized (None when not asked for)."""
 
-    __slots__ = ("q_labels", "k_labels", "q_sizes", "k_sizes", "q_idx", "k_idx", "pack")
+    __slots__ = ("q_labels", "k_labels", "q_sizes", "k_sizes", "q_idx", "k_idx", "pack", "q_hat")
 
-    def __init__(self, q_labels, k_labels, q_sizes, k_sizes, q_idx, k_idx, pack):
+    def __init__(self, q_labels, k_labels, q_sizes, k_sizes, q_idx, k_idx, pack, q_hat=None):
         self.q_labels, self.k_labels, self.q_sizes, self.k_sizes = q_labels, k_labels, q_sizes, k_sizes
-        self.q_idx, self.k_idx, self.pack = q_idx, k_idx, pack
+        self.q_idx, self.k_idx, self.pack, self.q_hat = q_idx, k_idx, pack, q_hat
 
 
 class PecoAttention:
@@ -161,14 +162,16 @@ class PecoAttention:
         fit = self._fit_clusters(query, key)
         return fit.q_labels, fit.k_labels, fit.q_sizes, fit.k_sizes
 
-    def _fit_clusters(self, query, key, pack_keys=None, pack_order="cluster"):
+    def _fit_clusters(self, query, key, pack_keys=None, pack_order="cluster", query_full=None):
         """``_update_cluster_state`` returning a _FitResult. With ``pack_keys = (bits, key_full,
         value_full)`` ([B,H,S,D], key the tensor whose video part is ``key``; value_full None
-        for ``pack_order="original"``) the last update also writes K Base-Offset
-        fake-quantized against its final centres, with the text rows after the video rows:
-        in the final key cluster order together with V, or each row at its own position
+        for ``pack_order="original"``) the fit also writes K Base-Offset fake-quantized
+        against its final centres, with the text rows after the video rows: in the final key
+        cluster order together with V, or each row at its own position
         (``pack_order="original"``, no V). A fourth entry ``True`` adds the keys' codes, lows
-        and scales in the same order. The result's ``pack`` holds these tensors.
+        and scales in the same order. The result's ``pack`` holds these tensors. With
+        ``pack_order="original"``, ``query_full`` ([B,H,S,D], the tensor whose video part is
+        ``query``) makes the fit write Q fake-quantized the same way (``q_hat``).
         """
         batch, heads, length, dim = query.shape
         initializing = self.q_centroids is None
@@ -185,7 +188,7 @@ class PecoAttention:
         k_init = self._initial_centers(k_flat, self.k_centroids, self.config.num_k_centroids)
         if q_flat.dtype not in (torch.float16, torch.bfloat16, torch.float32) or q_flat.dtype != k_flat.dtype:
             q_flat, k_flat = q_flat.float(), k_flat.float()
-        pack = None
+        pack = q_hat = None
         if pack_keys is None:
             problems = [clustering_cuda.KMeansProblem(q_flat, q_init), clustering_cuda.KMeansProblem(k_flat, k_init)]
             outs = clustering_cuda.kmeans_fit(problems, iterations)
@@ -200,19 +203,29 @@ class PecoAttention:
                 raise ValueError("the packed key and value must be contiguous [B,H,S,D] tensors like key")
             k_rows = key_full.reshape(batch * heads, full, dim)[:, :length]
             value_flat = None if value_full is None else value_full.reshape(batch * heads, full, dim)
+            q_pack = None
+            if query_full is not None:
+                if pack_order != "original" or query_full.shape != key_full.shape or \
+                        query_full.dtype != k_flat.dtype or not query_full.is_contiguous():
+                    raise ValueError("the packed query must be a contiguous [B,H,S,D] tensor like key, packed in "
+                                     "original order")
+                q_flat = query_full.reshape(batch * heads, full, dim)[:, :length]
+                q_pack = (bits, full, None)
             problems = [clustering_cuda.KMeansProblem(q_flat, q_init), clustering_cuda.KMeansProblem(k_rows, k_init)]
             outs, packed = clustering_cuda.kmeans_fit(problems, iterations,
-                                                      pack=[None, (bits, full, value_flat, with_codes)],
+                                                      pack=[q_pack, (bits, full, value_flat, with_codes)],
                                                       pack_order=pack_order)
             k_hat, v_perm = packed[1][:2]
             pack = (k_hat.view(batch, heads, full, dim),
                     None if v_perm is None else v_perm.view(batch, heads, full, dim), *packed[1][2:])
+            if q_pack is not None:
+                q_hat = packed[0][0].view(batch, heads, full, dim)
         (q_labels, q_cent, q_sizes, q_idx, _), (k_labels, k_cent, k_sizes, k_idx, _) = outs
         self.q_centroids, self.k_centroids = q_cent, k_cent
         if self.record_intermediates:
             self._last_fit, self._last_pack = (q_idx, k_idx), pack
         return _FitResult(q_labels, k_labels, q_sizes.reshape(batch, heads, -1), k_sizes.reshape(batch, heads, -1),
-                          q_idx, k_idx, pack)
+                          q_idx, k_idx, pack, q_hat)
 
     @staticmethod
     def _initial_centers(x, cached, clusters):
@@ -261,10 +274,11 @@ class PecoAttention:
             return base_offset_attention(query, k_perm, v_perm, dynamic_map, ext_q, ext_k, out_index=fit.q_idx,
                                          q_centroids=self.q_centroids, k_centroids=self.k_centroids,
                                          k_codes=k_codes, k_low=k_low, k_scale=k_scale, bits=bits)
-        # With Base-Offset on, the last k-means update also writes K fake-quantized, each row
-        # at its own position (stage 2 of K fused into the fit).
+        # With Base-Offset on, the fit ends with a launch that writes Q and K fake-quantized
+        # against their final centres, each row at its own position (stage 2 in the fit).
         fit = self._fit_clusters(query[:, :, :video_length], key[:, :, :video_length],
-                                 pack_keys=(bits, key, None) if bits else None, pack_order="original")
+                                 pack_keys=(bits, key, None) if bits else None, pack_order="original",
+                                 query_full=query if bits else None)
         # Cluster connectivity from the floating-point centres, extended with the text
         # partition (select_cluster_connections + extend_text_partition), in one launch that
         # also writes each query cluster's kept key segments and the attention's work items.
@@ -274,12 +288,11 @@ class PecoAttention:
             math.ceil(self.config.min_kc_ratio * self.config.num_k_centroids), (valid_text, text_length),
             length, length)
         # The attention reads Q/K/V through the sort permutations (stage 3 fused into its
-        # loads) and writes the output in original order, so no packed copy is made. With
-        # Base-Offset on, K comes fake-quantized from the fit and Q is fake-quantized as the
-        # attention loads it.
-        k_in = key if bits == 0 else fit.pack[0]
-        return sparse_attention_work(query, k_in, value, work, out_index=fit.q_idx, out_index_rows=video_length,
-                                     k_index=fit.k_idx, q_centroids=self.q_centroids if bits else None, bits=bits)
+        # loads) and writes the output in original order, so no cluster-order copy is made.
+        # With Base-Offset on, Q and K come fake-quantized from the fit.
+        q_in, k_in = (query, key) if bits == 0 else (fit.q_hat, fit.pack[0])
+        return sparse_attention_work(q_in, k_in, value, work, out_index=fit.q_idx, out_index_rows=video_length,
+                                     k_index=fit.k_idx)
 
     @torch.no_grad()
     def __call__(self, attn, hidden_states, encoder_hidden_states=None, attention_mask=None, image_rotary_emb=None):

@@ -1,12 +1,13 @@
 """Base-Offset fake quantization and the cluster gather fused into their neighbours.
 
-With Base-Offset on, the layer has no pack launch:
-- the k-means fit's last update writes K fake-quantized against the final centres, each row
-  at its own position with the text rows copied (peco_kmeans_fit_pack, hat_order 1; the
-  integer-score extension takes K and V in the final key-cluster order instead, hat_order 0);
-- the attention reads Q in its original order through the permutation and fake-quantizes it
-  as it loads the rows, and K/V through the key permutation (peco_sparse_attention_work with
-  q_centroids and k_index).
+With Base-Offset on, the layer has no cluster-order pack:
+- the k-means fit ends with a token-parallel launch that writes Q and K fake-quantized against
+  their final centres, each row at its own position with the text rows copied
+  (peco_kmeans_fit_pack, hat_order 1); the integer-score extension takes K and V in the final
+  key-cluster order from the last update instead (hat_order 0);
+- the attention reads Q, K and V through the permutations (peco_sparse_attention_work with
+  k_index). Its mode that fake-quantizes Q as it loads the rows (q_centroids) stays an entry
+  point of its own.
 All must equal the standalone pack launch (itself checked against the oracle's
 fake_quantize + gather + concat in test_gpu_stages.py) bit for bit, and the attention over
 them must equal the attention over packed inputs bit for bit.
@@ -154,5 +155,45 @@ def test_attention_quantizes_queries_with_indexed_keys(announce, dtype, d, bits)
                                                q_centroids=q_cent, bits=bits)
     out = attention_cuda.sparse_attention_work(q, k_hat, v, work, out_index=q_idx, out_index_rows=n,
                                                k_index=k_idx, q_centroids=q_cent, bits=bits)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("dtype,d,h,n,text,kq,kk,bits", [
+    (torch.bfloat16, 128, 3, 2000, 40, 12, 30, 4),
+    (torch.float16, 64, 2, 3000, 16, 10, 20, 8),
+    (torch.bfloat16, 128, 2, 1500, 0, 8, 24, 4),
+])
+def test_fit_packs_queries_and_keys_in_original_order(announce, dtype, d, h, n, text, kq, kk, bits):
+    """Both problems packed in original order (the Base-Offset layer's fit): each equals the
+    cluster-order pack launch scattered back through its permutation, and the attention over
+    the two fake-quantized tensors (indexed inputs) equals the attention that fake-quantizes Q
+    as it loads it, bit for bit."""
+    q, k, v, q_init, k_init = _fit_inputs(d + n + bits + 2, h, n, text, d, dtype, kq, kk)
+    length = n + text
+    announce(f"{dtype} D={d} H={h} N={n} text={text} KQ={kq} KK={kk} bits={bits}")
+    problems = [clustering_cuda.KMeansProblem(q[0, :, :n], q_init), clustering_cuda.KMeansProblem(k[0, :, :n], k_init)]
+    plain = clustering_cuda.kmeans_fit(problems, 2)
+    outs, packed = clustering_cuda.kmeans_fit(problems, 2, pack=[(bits, length, None), (bits, length, None)],
+                                              pack_order="original")
+    for a, b in zip(plain, outs):
+        for x, y in zip(a, b):
+            assert torch.equal(x, y)
+    for src, (labels, cent, _, idx, _), (hat, extra) in zip((q, k), outs, packed):
+        assert extra is None
+        (ref,) = clustering_cuda.pack_clustered([src], [idx], [labels], [cent], [bits], n)
+        expect = ref[0].clone()
+        expect[:, :n] = torch.empty_like(expect[:, :n]).scatter_(
+            1, idx.long()[..., None].expand(-1, -1, d), ref[0, :, :n])
+        torch.cuda.synchronize()
+        assert _bits_equal(hat.cpu(), expect.cpu())
+    (q_labels, q_cent, q_sizes, q_idx, _), (_, k_cent, k_sizes, k_idx, _) = outs
+    q_hat, k_hat = packed[0][0][None], packed[1][0][None]
+    work = clustering_cuda.select_work(q_cent[None], k_cent[None], q_sizes[None], k_sizes[None], 0.7, 4,
+                                       (max(text - 3, 0), text), length, length)
+    ref = attention_cuda.sparse_attention_work(q, k_hat, v, work, out_index=q_idx, out_index_rows=n,
+                                               k_index=k_idx, q_centroids=q_cent, bits=bits)
+    out = attention_cuda.sparse_attention_work(q_hat, k_hat, v, work, out_index=q_idx, out_index_rows=n,
+                                               k_index=k_idx)
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
