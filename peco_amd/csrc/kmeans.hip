@@ -1068,8 +1068,19 @@ __global__ __launch_bounds__(256) void km_pack_rows_kernel(KmArgs a, KmIter it) 
     const KmProblem& P = a.p[p];
     const int per_batch = static_cast<int>(ceil_div(P.length, R * U));
     const int local = static_cast<int>(blockIdx.x) - P.pack_begin;
-    const int b = local / per_batch;
-    const int t0 = (local % per_batch) * R * U + static_cast<int>(threadIdx.x) / G;
+    // Workgroup w runs on XCD w % kXcdCount. With a batch divisible by the XCD count (then so
+    // is every pack_begin), batch entry b's rows all go to XCD b % kXcdCount, so each XCD's L2
+    // fetches the centres of its own entries only.
+    int b, chunk;
+    if (P.batch % kXcdCount == 0) {
+        const int slot = local / kXcdCount;
+        b = local % kXcdCount + kXcdCount * (slot / per_batch);
+        chunk = slot % per_batch;
+    } else {
+        b = local / per_batch;
+        chunk = local % per_batch;
+    }
+    const int t0 = chunk * R * U + static_cast<int>(threadIdx.x) / G;
     const int sub = threadIdx.x % G;
     const int K = P.clusters;
     const float levels = static_cast<float>((1 << P.hat_bits) - 1);
