@@ -12,7 +12,10 @@ reconstructions. Checked here:
 - it is closer to that oracle than the kernel over rounded reconstructions is (a dropped or
   mis-signed term of the expansion would make it farther);
 - the layer with ``integer_scores`` stays within the tolerance of the reference's own layer
-  (peco_layer with bits=4: rounded reconstructions), for bf16 and fp16 inputs.
+  (peco_layer with bits=4: rounded reconstructions), for bf16 and fp16 inputs. This path is
+  outside the parity contract with the reference (it skips the rounding of the
+  reconstructions, peco/quantization.py:136); that last check is a bound on how far the
+  extension strays, and its margin is printed.
 """
 import numpy as np
 import pytest
@@ -149,5 +152,7 @@ def test_layer_with_integer_scores_matches_the_reference_layer(announce, dtype):
                               k_init=wl.k_init, top_p=wl.top_p, min_kc_ratio=wl.min_kc_ratio, bits=shape.bits,
                               text_length=shape.text, valid_text=shape.text, fit=fit)
     err = (out.float().cpu() - expected.float()).abs()
-    print(f"layer vs reference: max {err.max().item():.3e} mean {err.mean().item():.3e}", flush=True)
-    assert err.max().item() <= 2e-2 and err.mean().item() <= 2e-3
+    emax, emean = err.max().item(), err.mean().item()
+    print(f"layer vs reference: max {emax:.3e} ({emax / 2e-2:.0%} of the 2e-2 bound), "
+          f"mean {emean:.3e} ({emean / 2e-3:.0%} of 2e-3)", flush=True)
+    assert emax <= 2e-2 and emean <= 2e-3
