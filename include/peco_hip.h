@@ -84,10 +84,11 @@ int peco_kmeans_fit(int num_problems, const void* const* x, const int64_t* x_bat
                     const int* batch, const int* tokens, const int* clusters, int dims, int dtype, int iterations,
                     void* workspace, size_t workspace_bytes, void* stream);
 
-/* peco_kmeans_fit whose last update also packs (fuses peco/processor.py:141-149 into the
- * fit): for problem i with hat[i] non-null, hat[i] [batch, length, dims] receives x's rows
+/* peco_kmeans_fit that also packs (fuses peco/processor.py:141-149 into the fit): for
+ * problem i with hat[i] non-null, hat[i] [batch, length, dims] receives x's rows
  * Base-Offset fake-quantized with bits[i] (4 or 8) against the final centres, in the final
- * cluster order (hat_order 0) or each at its own token position (hat_order 1), then x's rows
+ * cluster order (hat_order 0, written by the last update) or each at its own token position
+ * (hat_order 1, written by one token-parallel launch after the last update), then x's rows
  * [tokens, length) unchanged (the text; x_batch_stride[i] must cover length rows);
  * with_in[i] -> with_out[i] ([batch, length, dims], both or neither, hat_order 0 only) are
  * gathered in the same order with their text rows copied. codes[i], low[i], scale[i] (all
