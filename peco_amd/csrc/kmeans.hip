@@ -1301,8 +1301,8 @@ struct KmFitDesc {
     int hat_order = 0;
 };
 
-// Workspace (bytes) for one problem.
-size_t km_workspace_bytes(int batch, int tokens, int clusters, int dims) {
+// Workspace (bytes) one problem's buffers take, each rounded up to 64 bytes.
+size_t km_workspace_raw(int batch, int tokens, int clusters, int dims) {
     const size_t bkd = static_cast<size_t>(batch) * clusters * dims;
     size_t bytes = 0;
     auto add = [&](size_t n) { bytes += (n + 63) / 64 * 64; };
@@ -1316,60 +1316,129 @@ size_t km_workspace_bytes(int batch, int tokens, int clusters, int dims) {
     return bytes;
 }
 
-// Two problems fit as two chains of launches, the second on a library-owned stream of the
-// current device (default priority), forked from and joined back to the caller's stream with
-// events, so one problem's memory-bound launches and the other's MFMA-bound ones overlap and
-// the launches' tails interleave (the 480p fit 0.69-0.70 ms against 0.72 ms in shared
-// launches). The stream and events are created once per device; the mutex keeps one
-// fork-join at a time per process on the host. If the stream cannot be made, the problems
-// share launches instead.
+// Workspace (bytes) for one problem: its buffers plus slack for the fit's halves, whose
+// buffers are rounded up separately (at most 64 bytes more per buffer).
+size_t km_workspace_bytes(int batch, int tokens, int clusters, int dims) {
+    return km_workspace_raw(batch, tokens, clusters, dims) + 64 * 16;
+}
+
+// A fit runs as up to four chains of launches: each problem's batch entries (heads) in two
+// halves, one chain on the caller's stream and the others on library-owned streams of the
+// current device (default priority), forked from the caller's stream with one event and
+// joined back to it with one event per side stream. One problem's memory-bound launches and
+// another's MFMA-bound ones then overlap and the launches' tails interleave: the 480p Q+K
+// fit takes 0.65-0.66 ms this way, 0.69-0.70 ms as two chains (one per problem) and 0.72 ms
+// with both problems sharing every launch. The streams and events are created once per
+// device; the mutex keeps one fork-join at a time per process on the host. If the streams
+// cannot be made, the problems share launches instead.
+constexpr int kFitParts = 2;                    // chains per problem (batch halves)
+constexpr int kSideStreams = kMaxKm * kFitParts - 1;
+
 struct SideStream {
     hipStream_t stream = nullptr;
     hipEvent_t fork = nullptr, join = nullptr;
 };
 
-bool side_stream(SideStream& out, std::mutex*& m) {
+bool side_streams(SideStream (&out)[kSideStreams], std::mutex*& m) {
     static std::mutex mutex;
-    static SideStream streams[64];
+    static SideStream streams[64][kSideStreams];
     int dev = -1;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
     std::lock_guard<std::mutex> lock(mutex);
-    SideStream& s = streams[dev];
-    if (!s.stream) {
-        if (hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking) != hipSuccess) return false;
-        if (hipEventCreateWithFlags(&s.fork, hipEventDisableTiming) != hipSuccess ||
-            hipEventCreateWithFlags(&s.join, hipEventDisableTiming) != hipSuccess)
-            return false;
+    for (int i = 0; i < kSideStreams; ++i) {
+        SideStream& s = streams[dev][i];
+        if (!s.stream) {
+            if (hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking) != hipSuccess) return false;
+            if (hipEventCreateWithFlags(&s.fork, hipEventDisableTiming) != hipSuccess ||
+                hipEventCreateWithFlags(&s.join, hipEventDisableTiming) != hipSuccess)
+                return false;
+        }
+        out[i] = s;
     }
-    out = s;
     m = &mutex;
     return true;
 }
 
-hipError_t km_fit(const KmFitDesc* descs, int num, int dims, int dtype, int iterations, void* workspace,
-                  float* sums, hipStream_t stream);
+// Batch entries [b0, b0 + nb) of a fit description (every pointer moved to entry b0).
+KmFitDesc slice_desc(const KmFitDesc& d, int b0, int nb, int dims, int dtype) {
+    KmFitDesc s = d;
+    const int64_t es = dtype == kF32 ? 4 : 2;
+    const int64_t xs = d.x_stride > 0 ? d.x_stride : static_cast<int64_t>(d.tokens) * dims;
+    const int64_t kd = static_cast<int64_t>(d.clusters) * dims;
+    const int64_t rows = static_cast<int64_t>(b0) * d.length * dims;  // packed rows of entries before b0
+    s.x = static_cast<const char*>(d.x) + b0 * xs * es;
+    s.x_stride = xs;
+    s.centers_in = d.centers_in + b0 * kd;
+    s.centers_out = d.centers_out + b0 * kd;
+    s.labels = d.labels + static_cast<int64_t>(b0) * d.tokens;
+    s.counts = d.counts + static_cast<int64_t>(b0) * d.clusters;
+    s.indices = d.indices + static_cast<int64_t>(b0) * d.tokens;
+    s.offsets = d.offsets + static_cast<int64_t>(b0) * (d.clusters + 1);
+    if (d.hat) s.hat = static_cast<char*>(d.hat) + rows * es;
+    if (d.with_in) s.with_in = static_cast<const char*>(d.with_in) + rows * es;
+    if (d.with_out) s.with_out = static_cast<char*>(d.with_out) + rows * es;
+    if (d.codes) s.codes = d.codes + static_cast<int64_t>(b0) * d.tokens * dims;
+    if (d.low) s.low = d.low + static_cast<int64_t>(b0) * d.tokens;
+    if (d.scale) s.scale = d.scale + static_cast<int64_t>(b0) * d.tokens;
+    s.batch = nb;
+    return s;
+}
 
-hipError_t km_fit_two_chains(const KmFitDesc* descs, int dims, int dtype, int iterations, void* workspace,
-                             hipStream_t stream, const SideStream& side, std::mutex& m) {
+hipError_t km_fit_launches(const KmFitDesc* descs, int num, int dims, int dtype, int iterations, void* workspace,
+                           float* sums, hipStream_t stream);
+
+// The chains of a fit (see above). The workspace holds each problem's slice of
+// km_workspace_bytes in turn; the halves of a problem take their parts of it in order (a
+// problem's size includes the slack for the extra rounding of two parts).
+hipError_t km_fit_chains(const KmFitDesc* descs, int num, int dims, int dtype, int iterations, void* workspace,
+                         hipStream_t stream, const SideStream (&side)[kSideStreams], std::mutex& m) {
     std::lock_guard<std::mutex> lock(m);
-    char* ws1 = static_cast<char*>(workspace) +
-                km_workspace_bytes(descs[0].batch, descs[0].tokens, descs[0].clusters, dims);
-    hipError_t e = hipEventRecord(side.fork, stream);
-    if (e == hipSuccess) e = hipStreamWaitEvent(side.stream, side.fork, 0);
-    if (e == hipSuccess) e = km_fit(&descs[1], 1, dims, dtype, iterations, ws1, nullptr, side.stream);
-    if (e == hipSuccess) e = hipEventRecord(side.join, side.stream);
-    if (e == hipSuccess) e = km_fit(&descs[0], 1, dims, dtype, iterations, workspace, nullptr, stream);
-    if (e == hipSuccess) e = hipStreamWaitEvent(stream, side.join, 0);
+    KmFitDesc parts[kMaxKm * kFitParts];
+    char* wsp[kMaxKm * kFitParts];
+    int n = 0;
+    char* ws = static_cast<char*>(workspace);
+    for (int q = 0; q < num; ++q) {
+        const KmFitDesc& d = descs[q];
+        char* w = ws;
+        for (int i = 0; i < kFitParts; ++i) {
+            const int b0 = d.batch * i / kFitParts, b1 = d.batch * (i + 1) / kFitParts;
+            parts[n] = slice_desc(d, b0, b1 - b0, dims, dtype);
+            wsp[n++] = w;
+            w += km_workspace_raw(b1 - b0, d.tokens, d.clusters, dims);
+        }
+        ws += km_workspace_bytes(d.batch, d.tokens, d.clusters, dims);
+    }
+    // The first half of the last problem (the larger one in the layer) on the caller's stream.
+    const int home = (num - 1) * kFitParts;
+    hipError_t e = hipEventRecord(side[0].fork, stream);
+    for (int i = 0; e == hipSuccess && i < n - 1; ++i) e = hipStreamWaitEvent(side[i].stream, side[0].fork, 0);
+    int si = 0;
+    for (int i = 0; e == hipSuccess && i < n; ++i) {
+        if (i == home) continue;
+        e = km_fit_launches(&parts[i], 1, dims, dtype, iterations, wsp[i], nullptr, side[si].stream);
+        if (e == hipSuccess) e = hipEventRecord(side[si].join, side[si].stream);
+        ++si;
+    }
+    if (e == hipSuccess) e = km_fit_launches(&parts[home], 1, dims, dtype, iterations, wsp[home], nullptr, stream);
+    for (int i = 0; e == hipSuccess && i < n - 1; ++i) e = hipStreamWaitEvent(stream, side[i].join, 0);
     return e;
 }
 
 hipError_t km_fit(const KmFitDesc* descs, int num, int dims, int dtype, int iterations, void* workspace,
                   float* sums, hipStream_t stream) {
-    if (num == 2) {
-        SideStream side;
+    bool split = !sums;  // the sums output of a one-problem fit is not sliced
+    for (int q = 0; q < num; ++q) split = split && descs[q].batch >= kFitParts;
+    if (split) {
+        SideStream side[kSideStreams];
         std::mutex* m = nullptr;
-        if (side_stream(side, m)) return km_fit_two_chains(descs, dims, dtype, iterations, workspace, stream, side, *m);
+        if (side_streams(side, m)) return km_fit_chains(descs, num, dims, dtype, iterations, workspace, stream, side, *m);
     }
+    return km_fit_launches(descs, num, dims, dtype, iterations, workspace, sums, stream);
+}
+
+// One chain of launches for every problem together (the problems share each launch).
+hipError_t km_fit_launches(const KmFitDesc* descs, int num, int dims, int dtype, int iterations, void* workspace,
+                           float* sums, hipStream_t stream) {
     KmArgs a{};
     SortArgs sa{};
     a.num = num;
