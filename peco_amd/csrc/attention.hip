@@ -289,11 +289,12 @@ __device__ __forceinline__ void load_tile_lds(uint16_t* ks, uint16_t* vs, const 
             const int i = i0 + j;
             const int r = (i * NL + first) * T::kWaveRows + lane / T::CH;  // tile row written by this lane
             const int p = lane % T::CH;                                        // physical chunk
-            const int64_t g = static_cast<int64_t>(rows[j]) * D;
+            // Byte offsets within the head (rows < 2^31 / (2 D) there, so 32 bits suffice).
+            const uint32_t g = static_cast<uint32_t>(rows[j]) * (D * 2);
             const uint32_t kdst = lds_base + static_cast<uint32_t>(((i * NL) * kWave * 8) * 2);
             const uint32_t vdst = kdst + vs_delta;
-            dma16(kh + g + (p ^ T::swz_k(r)) * 8, kdst);
-            dma16(vh + g + (p ^ T::swz_v(r)) * 8, vdst);
+            dma16_off(kh, g + (p ^ T::swz_k(r)) * 16, kdst);
+            dma16_off(vh, g + (p ^ T::swz_v(r)) * 16, vdst);
         }
     }
 #endif

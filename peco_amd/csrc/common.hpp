@@ -121,6 +121,12 @@ __device__ __forceinline__ void dma16(const uint16_t* src, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
 }
 
+// The same with a wave-uniform base address in SGPRs and a 32-bit byte offset per lane (one
+// VALU operation per load for the offset instead of 64-bit address arithmetic).
+__device__ __forceinline__ void dma16_off(const void* base, uint32_t off, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds) : "memory", "m0");
+}
+
 // The same with 4 bytes per lane: lane i writes lds + 4i.
 __device__ __forceinline__ void dma4(const void* src, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
