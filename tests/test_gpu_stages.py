@@ -209,6 +209,7 @@ def test_update_lockstep_fp32(announce, dims):
     (torch.bfloat16, 64, 4000, 10, 1000, 3),   # fused, clusters span four 256-thread passes
     (torch.bfloat16, 64, 9000, 16, 40, 4),     # 36 tiles: scan + place
     (torch.bfloat16, 64, 5000, 16, 1100, 3),   # 1100 clusters: scan + place
+    (torch.bfloat16, 128, 6000, 24, 600, 4),   # D = 128 with 600 centres, duplicated ones among them
 ])
 def test_fused_fit_bit_exact(announce, dtype, dims, n, kq, kk, iters):
     g = _gen(n + kq)
