@@ -358,8 +358,13 @@ __device__ __forceinline__ void attention_item(
     const int slot = in_band / band;
     if (slot >= counts[bh]) return;
     const int32_t* item = items + (static_cast<int64_t>(bh) * cap + slot) * 3;
-    const int q_start = item[0], qc = item[1], q_rows = item[2];
-    const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave, h = lane / 32;
+    // Values every lane loads alike are moved to scalar registers (readfirstlane), so the
+    // branches on them are wave-uniform.
+    const int q_start = __builtin_amdgcn_readfirstlane(item[0]);
+    const int qc = __builtin_amdgcn_readfirstlane(item[1]);
+    const int q_rows = __builtin_amdgcn_readfirstlane(item[2]);
+    const int tid = threadIdx.x, lane = tid % kWave, h = lane / 32;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int64_t head = static_cast<int64_t>(bh);
     const uint32_t sq_last = static_cast<uint32_t>(sq - 1), sk_last = static_cast<uint32_t>(sk - 1);
 
@@ -444,6 +449,8 @@ __device__ __forceinline__ void attention_item(
         if (tid == 0) kseg[nk] = int2{0, 0x7fffffff};
     }
     __syncthreads();
+    L = __builtin_amdgcn_readfirstlane(L);
+    nk = __builtin_amdgcn_readfirstlane(nk);
     const int ntiles = static_cast<int>(ceil_div(L, kKTile));
     // Physical row of stream row r (r < L). Every lane asks for increasing rows (its row of
     // every tile), so a forward-only cursor over the segments suffices.
