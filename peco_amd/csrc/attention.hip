@@ -6,15 +6,17 @@
 //
 // Work list (one 256-thread workgroup per (batch*head)):
 //   cluster offsets are min(S, prefix of max(0, size)) (the reference's clamped running sum),
-//   each query cluster is cut into items of <= 128 rows, and the items of one head are
-//   ordered by descending cost rows * kept_keys. The attention grid is slot-major over bands
+//   each query cluster is cut into items of <= 128 rows (256 from 65536 query rows on), and the
+//   items of one head are ordered by descending cost rows * kept_keys. The attention grid is
+//   slot-major over bands
 //   of heads (block = band_index * band * cap + slot * band + head in band): the costliest
 //   item of every head of a band starts first. The band is all heads when their K/V take at
 //   most 96 MB (then, with BH a multiple of 8, all items of one head land on one XCD, whose L2
 //   holds that head's K/V), else up to four heads whose K/V fit in the MALL, so long
 //   sequences re-read each head's K/V from the MALL instead of HBM.
 //
-// Attention workgroup = one item: 4 waves x 32 query rows. The kept key clusters of the
+// Attention workgroup = one item: 4 waves x 32 query rows (8 waves x 32 rows for the 256-row
+// items of long sequences, see attention_item_rows in work.hpp). The kept key clusters of the
 // item's query cluster form one virtual key stream (their rows are contiguous per cluster
 // after the sort); it is processed in 64-key tiles gathered into LDS, so ragged clusters
 // cost no masked MFMA work except the stream's last partial tile.
@@ -38,7 +40,6 @@ namespace peco {
 namespace {
 
 constexpr int kKTile = 64;    // keys per LDS tile
-constexpr int kSplitRows = 64;  // items up to this many rows pair their waves
 
 struct WorkLayout {
     int32_t* counts;   // [bh]
@@ -68,7 +69,7 @@ __global__ __launch_bounds__(256) void build_work_kernel(const uint8_t* __restri
                                                          const int* __restrict__ q_sizes,
                                                          const int* __restrict__ k_sizes,
                                                          const int32_t* __restrict__ kept_in, int32_t* ws, int bhn,
-                                                         int sq, int sk, int cq, int ck) {
+                                                         int sq, int sk, int cq, int ck, int tile) {
     extern __shared__ int lds[];
     __shared__ int tmp[4];
     const int bh = blockIdx.x;
@@ -207,7 +208,8 @@ __global__ __launch_bounds__(256) void build_work_kernel(const uint8_t* __restri
         }
     }
     __syncthreads();
-    order_head_items<4>(qoff, kept, cq, W.items + static_cast<int64_t>(bh) * W.cap * 3, W.counts + bh, keys, tmp);
+    order_head_items<4>(qoff, kept, cq, tile, W.items + static_cast<int64_t>(bh) * W.cap * 3, W.counts + bh, keys,
+                        tmp);
 }
 
 template <int DT> struct Mfma;
@@ -320,8 +322,9 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 // is null, from the item's map row and the clamped key-cluster prefix kprefix [bh, ck + 1].
 enum InputMode : int { kPacked = 0, kIndexed = 1, kQuantQ = 2, kIndexedQuantQ = 3 };
 
-// One work item (linear index g over bands x slots x heads, see below) of the attention.
-template <int DT, int D, int kMode>
+// One work item (linear index g over bands x slots x heads, see below) of the attention, run
+// by a workgroup of kWaves wavefronts (4, or 8 for the items of 2 * kQTile rows).
+template <int DT, int D, int kMode, int kWaves>
 __device__ __forceinline__ void attention_item(
     int g, const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint8_t* __restrict__ selected, const int32_t* __restrict__ kprefix, const int2* __restrict__ segs,
@@ -338,13 +341,16 @@ __device__ __forceinline__ void attention_item(
     constexpr float kLazyLog2 = 8.0f;
     // K tiles (buffers 0, 1) and V tiles (2, 3) in one array: after the last tile the paired
     // waves exchange their softmax states through it, which takes more than the K half.
+    constexpr int NT = kWaves * kWave;           // threads of the workgroup
+    constexpr int H = kWaves / 2;                // row blocks of a paired (split) item
+    constexpr int kRowsPerWave = kKTile / kWaves;  // tile rows whose physical row a wave looks up
     __shared__ __align__(16) uint16_t kvs[4][T::kElems];
     uint16_t(*const ks)[T::kElems] = kvs;
     uint16_t(*const vs)[T::kElems] = kvs + 2;
     static_assert(2 * kWave * (NB * 16 + 2) * sizeof(float) <= sizeof(kvs), "pair exchange exceeds the tile LDS");
     __shared__ int prow[2][kKTile];
     __shared__ int pidx[2][kKTile];    // k_index values of tile t+3 rows (indexed inputs)
-    __shared__ int tmp[4];
+    __shared__ int tmp[kWaves];
     extern __shared__ int dyn[];
     // Key stream of this query cluster: the kept, non-empty key clusters in order. Segment i
     // is {first physical row - stream offset, stream offset} of the i-th of them, followed by
@@ -368,22 +374,28 @@ __device__ __forceinline__ void attention_item(
     const int64_t head = static_cast<int64_t>(bh);
     const uint32_t sq_last = static_cast<uint32_t>(sq - 1), sk_last = static_cast<uint32_t>(sk - 1);
 
-    // Items of at most kSplitRows rows pair the waves: wave w takes 32-row block w & 1 and, of
-    // every tile, only the 32-key half w >> 1, so a short item's tiles cost about half the
+    // Items of at most 32 * H rows pair the waves: wave w takes 32-row block w % H and, of
+    // every tile, only the 32-key half w / H, so a short item's tiles cost about half the
     // time; each pair merges its two partial softmax states after the last tile. Longer items
     // give each wave its own row block and both halves of every tile.
-    const bool split = q_rows <= kSplitRows;
-    const int rb = split ? (wave & 1) : wave;  // this wave's 32-row block
-    const int hb = split ? (wave >> 1) : 0;    // first 32-key half this wave processes
+    const bool split = q_rows <= 32 * H;
+    const int rb = split ? (wave % H) : wave;  // this wave's 32-row block
+    const int hb = split ? (wave / H) : 0;     // first 32-key half this wave processes
     // Waves without query rows issue every tile load, so that waiting for the load path to
-    // accept them never delays a wave with MFMA work; with no such wave all four share.
+    // accept them never delays a wave with MFMA work; with no such wave all of them share.
     const int row_blocks = static_cast<int>(ceil_div(q_rows, 32));
-    const int idle = split ? 4 - 2 * row_blocks : 4 - row_blocks;   // waves 4-idle .. 3 (or 1, 3)
-    const int loaders = idle >= 2 ? 2 : (idle == 1 ? 1 : 4);
+    const int idle = split ? kWaves - 2 * row_blocks : kWaves - row_blocks;
+    const int loaders = idle >= 4 ? 4 : (idle >= 2 ? 2 : (idle == 1 ? 1 : kWaves));
     int loader_rank;
-    if (loaders == 4) loader_rank = wave;
-    else if (split) loader_rank = (wave & 1) ? wave >> 1 : -1;   // idle waves 1 and 3
-    else loader_rank = wave >= 4 - loaders ? wave - (4 - loaders) : -1;
+    if (loaders == kWaves) {
+        loader_rank = wave;
+    } else if (split) {
+        // Idle waves hold row blocks row_blocks .. H-1 of either key half.
+        const int r = rb >= row_blocks ? (wave / H) * (H - row_blocks) + (rb - row_blocks) : -1;
+        loader_rank = r < loaders ? r : -1;
+    } else {
+        loader_rank = wave >= kWaves - loaders ? wave - (kWaves - loaders) : -1;
+    }
     // Q^T operand: lane holds query row (32*rb + l%32), channels 16s + 8h .. +7. Its loads
     // (and the permutation entry they depend on) go out before the key stream's, so their
     // latency overlaps the stream setup below.
@@ -422,11 +434,11 @@ __device__ __forceinline__ void attention_item(
         nk = min(max(hdr.x, 0), ck);
         L = max(hdr.y, 0);
         if (tid <= nk) kseg[tid] = first;
-        for (int i = tid + 256; i <= nk; i += 256) kseg[i] = srow[1 + i];
+        for (int i = tid + NT; i <= nk; i += NT) kseg[i] = srow[1 + i];
     } else {
         const uint8_t* sel = selected + (static_cast<int64_t>(bh) * cq + qc) * ck;
         const int32_t* gk = kprefix + static_cast<int64_t>(bh) * (ck + 1);
-        const int per = static_cast<int>(ceil_div(ck, 256));
+        const int per = static_cast<int>(ceil_div(ck, NT));
         const int c0 = tid * per, c1 = min(ck, c0 + per);
         int local = 0, lcount = 0;
         for (int c = c0; c < c1; ++c) {
@@ -436,8 +448,8 @@ __device__ __forceinline__ void attention_item(
                 ++lcount;
             }
         }
-        int run = block_scan<4>(local, tmp, &L);
-        int idx = block_scan<4>(lcount, tmp, &nk);
+        int run = block_scan<kWaves>(local, tmp, &L);
+        int idx = block_scan<kWaves>(lcount, tmp, &nk);
         for (int c = c0; c < c1; ++c) {
             const int a = gk[c], e = gk[c + 1];
             if (sel[c] && e > a) {
@@ -474,8 +486,8 @@ __device__ __forceinline__ void attention_item(
     // goes straight to LDS (no register is written behind the compiler's back), so the loop
     // waits for them explicitly.
     const int32_t* kidx = kIndexedKV ? k_index + head * oi_rows : nullptr;
-    const int prow_entry = 16 * wave + lane % 16;
-    const bool prow_owner = lane < 16;
+    const int prow_entry = kRowsPerWave * wave + lane % kRowsPerWave;
+    const bool prow_owner = lane < kRowsPerWave;
     // Stream position (cluster-order row) of stream row r; rows past the stream read row 0.
     auto stream_pos = [&](int r) { return r < L ? static_cast<int>(min(static_cast<uint32_t>(row_of(r)), sk_last)) : 0; };
     // Physical row of stream position p, given k_index[p] (clamped to the head's rows, so a bad
@@ -627,7 +639,7 @@ __device__ __forceinline__ void attention_item(
 #endif
     }
     __syncthreads();
-    if (ntiles > 0) load_tile_lds<D, 4>(ks[0], vs[0], kh, vh, prow[0], wave, lane);
+    if (ntiles > 0) load_tile_lds<D, kWaves>(ks[0], vs[0], kh, vh, prow[0], wave, lane);
     if constexpr (kQuantLoad) {
         if (qc < qcent_rows) {
             // This lane holds channels 16s + 8h .. +7 of its row and lane l ^ 32 the others:
@@ -662,10 +674,11 @@ __device__ __forceinline__ void attention_item(
     auto step = [&](auto bufc, int tile) __attribute__((always_inline)) {
         constexpr int buf = decltype(bufc)::value;
         const bool more = tile + 1 < ntiles;
-        // Waves with rows only ever load as one of four loaders (the other counts mean idle
-        // waves carry the loads).
+        // Waves with rows only ever load as one of all kWaves loaders (the other counts mean
+        // idle waves carry the loads).
         auto shared_load = [&]() __attribute__((always_inline)) {
-            if (more && loaders == 4) load_tile_lds<D, 4>(ks[buf ^ 1], vs[buf ^ 1], kh, vh, prow[buf ^ 1], wave, lane);
+            if (more && loaders == kWaves)
+                load_tile_lds<D, kWaves>(ks[buf ^ 1], vs[buf ^ 1], kh, vh, prow[buf ^ 1], wave, lane);
         };
         if (wave_active) {
             // Key half hb (with the next tile's loads issued behind its S^T MFMAs), then, for
@@ -673,13 +686,14 @@ __device__ __forceinline__ void attention_item(
             compute(std::integral_constant<int, 1>{}, hb, ks[buf], vs[buf], tile * kKTile, shared_load);
             if (!split) compute(std::integral_constant<int, 1>{}, 1, ks[buf], vs[buf], tile * kKTile, [] {});
         } else if (more && loader_rank >= 0) {
-            if (loaders == 4) load_tile_lds<D, 4>(ks[buf ^ 1], vs[buf ^ 1], kh, vh, prow[buf ^ 1], wave, lane);
+            if (loaders == kWaves) load_tile_lds<D, kWaves>(ks[buf ^ 1], vs[buf ^ 1], kh, vh, prow[buf ^ 1], wave, lane);
+            else if (loaders == 4) load_tile_lds<D, 4>(ks[buf ^ 1], vs[buf ^ 1], kh, vh, prow[buf ^ 1], loader_rank, lane);
             else if (loaders == 2) load_tile_lds<D, 2>(ks[buf ^ 1], vs[buf ^ 1], kh, vh, prow[buf ^ 1], loader_rank, lane);
             else load_tile_lds<D, 1>(ks[buf ^ 1], vs[buf ^ 1], kh, vh, prow[buf ^ 1], loader_rank, lane);
         }
         if constexpr (kIndexedKV) {
             const int p3 = stream_pos((tile + 3) * kKTile + prow_entry);
-            if (prow_owner) dma4(kidx + min(p3, oi_rows - 1), lds_addr(&pidx[buf][16 * wave]));
+            if (prow_owner) dma4(kidx + min(p3, oi_rows - 1), lds_addr(&pidx[buf][kRowsPerWave * wave]));
             // Everything but that index load has landed: this wave's tile t+1 loads and the
             // index loaded a tile ago (pidx[buf ^ 1]).
             asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
@@ -704,30 +718,36 @@ __device__ __forceinline__ void attention_item(
         // Merge the pair's states: the second-half wave (hb = 1) leaves m, l and O in the tile
         // LDS (the K and V buffers, free after the loop's last barrier), the first-half wave
         // rescales both to the larger maximum and adds. Lane l of both waves holds the same
-        // query rows.
-        float* xch = reinterpret_cast<float*>(&kvs[0][0]) + (rb * kWave + lane) * (NB * 16 + 2);
-        if (hb == 1 && wave_active) {
+        // query rows. The LDS holds the states of two row blocks at a time, so the H row blocks
+        // of an 8-wavefront item take turns in pairs.
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
+        for (int r0 = 0; r0 < H; r0 += 2) {
+            const bool turn = rb >= r0 && rb < r0 + 2;
+            float* xch = reinterpret_cast<float*>(&kvs[0][0]) + ((rb - r0) * kWave + lane) * (NB * 16 + 2);
+            if (turn && hb == 1 && wave_active) {
 #pragma unroll
-                for (int i = 0; i < 16; ++i) xch[nb * 16 + i] = oacc[nb][i];
-            xch[NB * 16] = m_run;
-            xch[NB * 16 + 1] = l_run;
+                for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) xch[nb * 16 + i] = oacc[nb][i];
+                xch[NB * 16] = m_run;
+                xch[NB * 16 + 1] = l_run;
+            }
+            __syncthreads();
+            if (turn && hb == 0 && wave_active) {
+                const float m1 = xch[NB * 16], l1 = xch[NB * 16 + 1];
+                const float m = fmaxf(m_run, m1);
+                // A half without keys has m = -inf (and l = 0, O = 0); both empty leaves O at 0.
+                const float a0 = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_run - m) * scale_log2);
+                const float a1 = m1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m1 - m) * scale_log2);
+                l_run = l_run * a0 + l1 * a1;
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) oacc[nb][i] = oacc[nb][i] * a0 + xch[nb * 16 + i] * a1;
+            }
+            if (r0 + 2 < H) __syncthreads();  // the next pair's states overwrite these
         }
-        __syncthreads();
         if (hb == 1) return;
-        if (wave_active) {
-            const float m1 = xch[NB * 16], l1 = xch[NB * 16 + 1];
-            const float m = fmaxf(m_run, m1);
-            // A half without keys has m = -inf (and l = 0, O = 0); both empty leaves O at 0.
-            const float a0 = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_run - m) * scale_log2);
-            const float a1 = m1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m1 - m) * scale_log2);
-            l_run = l_run * a0 + l1 * a1;
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) oacc[nb][i] = oacc[nb][i] * a0 + xch[nb * 16 + i] * a1;
-        }
     }
     if (!qvalid) return;
     const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
@@ -784,8 +804,8 @@ __device__ int resolve_item(int32_t* queues, const int32_t* counts, int cap, int
     return -1;
 }
 
-template <int DT, int D, int kMode, bool kPersist>
-__global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
+template <int DT, int D, int kMode, bool kPersist, int kWaves>
+__global__ __launch_bounds__(kWaves * kWave, 8 / kWaves) void sparse_attention_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint8_t* __restrict__ selected, const int32_t* __restrict__ kprefix, const int2* __restrict__ segs,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ items, int cap, uint16_t* __restrict__ out,
@@ -793,9 +813,9 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
     const float* __restrict__ qcent, int qcent_rows, float levels, int bhn, int band, int sq, int sk, int cq,
     int ck, float scale_log2, int32_t* __restrict__ queues, int nwg) {
     if constexpr (!kPersist) {
-        attention_item<DT, D, kMode>(blockIdx.x, q, k, v, selected, kprefix, segs, counts, items, cap, out, out_index,
-                                     oi_rows, k_index, qcent, qcent_rows, levels, bhn, band, sq, sk, cq, ck,
-                                     scale_log2);
+        attention_item<DT, D, kMode, kWaves>(blockIdx.x, q, k, v, selected, kprefix, segs, counts, items, cap, out,
+                                             out_index, oi_rows, k_index, qcent, qcent_rows, levels, bhn, band, sq,
+                                             sk, cq, ck, scale_log2);
     } else {
         __shared__ int next;
         const int total = cap * bhn;
@@ -810,9 +830,9 @@ __global__ __launch_bounds__(256, 2) void sparse_attention_kernel(
             __syncthreads();  // every wavefront has read `next` before thread 0 writes it again
             if (g < 0) break;
             x = g % kItemQueues;
-            attention_item<DT, D, kMode>(g, q, k, v, selected, kprefix, segs, counts, items, cap, out, out_index,
-                                         oi_rows, k_index, qcent, qcent_rows, levels, bhn, band, sq, sk, cq, ck,
-                                         scale_log2);
+            attention_item<DT, D, kMode, kWaves>(g, q, k, v, selected, kprefix, segs, counts, items, cap, out,
+                                                 out_index, oi_rows, k_index, qcent, qcent_rows, levels, bhn, band, sq,
+                                                 sk, cq, ck, scale_log2);
         }
         if (threadIdx.x == 0 && atomicAdd(&queues[kItemQueues], 1) == nwg - 1) {
             for (int x = 0; x <= kItemQueues; ++x)
@@ -1321,7 +1341,11 @@ int launch_attention_kernel(const void* q, const void* k, const void* v, const u
     const size_t lds_attn = sizeof(int) * 2 * (static_cast<size_t>(ck) + 1);
     const float scale_log2 = static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(d)));
     const int64_t total = static_cast<int64_t>(cap) * bh;
-    const int nwg = static_cast<int>(std::min<int64_t>(total, 2 * static_cast<int64_t>(device_compute_units())));
+    // Items of 2 * kQTile rows (attention_item_rows, the builders' rule) run on 8-wavefront
+    // workgroups, one per CU; others on 4-wavefront ones, two per CU.
+    const int waves = attention_item_rows(sq) == 2 * kQTile ? 8 : 4;
+    const int nwg = static_cast<int>(
+        std::min<int64_t>(total, (8 / waves) * static_cast<int64_t>(device_compute_units())));
     if (queues && total < static_cast<int64_t>(kPersistItems) * nwg) queues = nullptr;
     const dim3 grid(static_cast<unsigned>(queues ? nwg : total));
     const int band = attention_head_band(bh, sk, d);
@@ -1329,19 +1353,24 @@ int launch_attention_kernel(const void* q, const void* k, const void* v, const u
     const auto* kp = static_cast<const uint16_t*>(k);
     const auto* vp = static_cast<const uint16_t*>(v);
     auto* op = static_cast<uint16_t*>(output);
-#define PECO_ATTN_P(DT_, D_, M_, P_)                                                                               \
-    hipLaunchKernelGGL((sparse_attention_kernel<DT_, D_, M_, P_>), grid, dim3(256), lds_attn, s, qp, kp, vp,        \
-                       selected, kprefix, segs, counts, items, cap, op, out_index, out_index_rows, k_index,          \
+#define PECO_ATTN_P(DT_, D_, M_, P_, W_)                                                                           \
+    hipLaunchKernelGGL((sparse_attention_kernel<DT_, D_, M_, P_, W_>), grid, dim3(W_ * kWave), lds_attn, s, qp, kp, \
+                       vp, selected, kprefix, segs, counts, items, cap, op, out_index, out_index_rows, k_index,      \
                        q_centroids, q_clusters, levels, bh, band, sq, sk, cq, ck, scale_log2, queues, nwg)
-#define PECO_ATTN(DT_, D_, M_)                                                                                     \
+#define PECO_ATTN(DT_, D_, M_, W_)                                                                                 \
     do {                                                                                                           \
-        if (queues) PECO_ATTN_P(DT_, D_, M_, true);                                                                \
-        else PECO_ATTN_P(DT_, D_, M_, false);                                                                      \
+        if (queues) PECO_ATTN_P(DT_, D_, M_, true, W_);                                                            \
+        else PECO_ATTN_P(DT_, D_, M_, false, W_);                                                                  \
+    } while (0)
+#define PECO_ATTN_W(DT_, D_, M_)                                                                                   \
+    do {                                                                                                           \
+        if (waves == 8) PECO_ATTN(DT_, D_, M_, 8);                                                                 \
+        else PECO_ATTN(DT_, D_, M_, 4);                                                                            \
     } while (0)
 #define PECO_ATTN_D(DT_, M_)                                                                                       \
     do {                                                                                                           \
-        if (d == 128) PECO_ATTN(DT_, 128, M_);                                                                     \
-        else PECO_ATTN(DT_, 64, M_);                                                                               \
+        if (d == 128) PECO_ATTN_W(DT_, 128, M_);                                                                   \
+        else PECO_ATTN_W(DT_, 64, M_);                                                                             \
     } while (0)
 #define PECO_ATTN_M(DT_)                                                                                           \
     do {                                                                                                           \
@@ -1354,6 +1383,7 @@ int launch_attention_kernel(const void* q, const void* k, const void* v, const u
     else PECO_ATTN_M(kF16);
 #undef PECO_ATTN_M
 #undef PECO_ATTN_D
+#undef PECO_ATTN_W
 #undef PECO_ATTN
 #undef PECO_ATTN_P
     return hipGetLastError();
@@ -1379,10 +1409,10 @@ int launch_sparse_attention(const void* q, const void* k, const void* v, const u
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (kept_keys)
         hipLaunchKernelGGL(build_work_kernel<true>, dim3(bh), dim3(256), lds_build, s, selected, q_sizes, k_sizes,
-                           kept_keys, workspace, bh, sq, sk, cq, ck);
+                           kept_keys, workspace, bh, sq, sk, cq, ck, attention_item_rows(sq));
     else
         hipLaunchKernelGGL(build_work_kernel<false>, dim3(bh), dim3(256), lds_build, s, selected, q_sizes, k_sizes,
-                           nullptr, workspace, bh, sq, sk, cq, ck);
+                           nullptr, workspace, bh, sq, sk, cq, ck, attention_item_rows(sq));
     const WorkLayout W = work_layout(workspace, bh, sq, cq, ck);
     return launch_attention_kernel(q, k, v, selected, W.kprefix, nullptr, W.counts, W.items, W.cap, output, out_index,
                                    out_index_rows, k_index, nullptr, 0, 0, bh, sq, sk, d, cq, ck, dtype, nullptr, s);
@@ -1475,8 +1505,9 @@ PECO_API int peco_base_offset_attention(const void* q, const int32_t* out_index,
     const size_t lds_list = sizeof(int) * 3 * static_cast<size_t>(ck);
     if (lds_build > 60 * 1024 || lds_list > 24 * 1024) return kUnsupportedShape;
     const hipStream_t s = static_cast<hipStream_t>(stream);
+    // The integer-score kernel runs 4-wavefront workgroups: items of kQTile rows.
     hipLaunchKernelGGL(build_work_kernel<false>, dim3(bh), dim3(256), lds_build, s, selected, q_sizes, k_sizes, nullptr,
-                       workspace, bh, sq, sk, cq, ck);
+                       workspace, bh, sq, sk, cq, ck, kQTile);
     const WorkLayout W = work_layout(workspace, bh, sq, cq, ck);
     BoAttnArgs a;
     a.q = static_cast<const uint16_t*>(q);

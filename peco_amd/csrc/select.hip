@@ -424,8 +424,8 @@ __global__ __launch_bounds__(kSelWaves * kWave) void select_kernel(
             kept[r] = max(0, __hip_atomic_load(work.row_keys + static_cast<int64_t>(b) * re + r, __ATOMIC_RELAXED,
                                                __HIP_MEMORY_SCOPE_AGENT));
         __syncthreads();
-        order_head_items<kSelWaves>(qoff, kept, re, work.items + static_cast<int64_t>(b) * work.cap * 3,
-                                    work.counts + b, keys, tmp);
+        order_head_items<kSelWaves>(qoff, kept, re, attention_item_rows(sq),
+                                    work.items + static_cast<int64_t>(b) * work.cap * 3, work.counts + b, keys, tmp);
         if (threadIdx.x == 0) work.tickets[b] = 0;  // ready for the next call
     }
 }

@@ -5,7 +5,8 @@ head, the attention items in cost order. Checked here against what the map defin
 - expanding a row's segments gives exactly the physical key rows of its kept clusters in
   cluster order (clamped cluster offsets, as the attention's own builder computes them), and
   segments are maximal (physically adjacent kept clusters share one);
-- the items are every query cluster cut into chunks of at most 128 rows, ordered by
+- the items are every query cluster cut into chunks of at most 128 rows (256 when the query
+  length is at least 65536: 8-wavefront attention workgroups), ordered by
   descending cost rows x stream length (cluster order beyond 2048 items), the builder's rule;
 - the attention over this work list equals, bit for bit, the map-driven attention on the
   same inputs (indexed and packed inputs);
@@ -58,11 +59,12 @@ def _segment_rows(seg_row):
 
 def _expected_items(qsizes, lengths, sq):
     qoff = _clamped_offsets(qsizes, sq)
+    tile = 256 if sq >= 65536 else 128
     entries = []
     for c in range(len(qsizes)):
         rows = int(qoff[c + 1] - qoff[c])
-        for ri, r in enumerate(range(0, rows, 128)):
-            n = min(128, rows - r)
+        for ri, r in enumerate(range(0, rows, tile)):
+            n = min(tile, rows - r)
             entries.append((min(n * int(lengths[c]), INT_MAX), c, ri, int(qoff[c]) + r, n))
     if len(entries) <= 2048:
         entries.sort(key=lambda e: (-e[0], e[1], e[2]))
@@ -232,20 +234,22 @@ def test_overwritten_work_list_is_rejected(announce):
     assert torch.equal(out, ref)
 
 
-@pytest.mark.parametrize("indexed", [True, False])
-def test_persistent_grid_equals_map_attention(announce, indexed):
-    """A launch with at least 8 item slots per resident workgroup (16 heads x 32896 rows, 130 x
-    514 extended map: 387 slots per head) runs the persistent grid, whose workgroups take items
-    from one queue per XCD; it must equal the map-driven attention (one workgroup per item) bit
-    for bit, twice on one work list (the first call resets the queues for the second)."""
-    h, cq, ck, video, text, valid, d = 16, 128, 512, 32640, 256, 200, 64
-    q, k, v, qs, ks, qidx, kidx, qc, kc = _clustered_inputs(7 + indexed, h, cq, ck, video, text, d, torch.bfloat16)
+def _persistent_case(announce, seed, h, cq, ck, video, text, valid, d, indexed, check_items):
+    q, k, v, qs, ks, qidx, kidx, qc, kc = _clustered_inputs(seed, h, cq, ck, video, text, d, torch.bfloat16)
     length = video + text
-    announce(f"H={h} N={video} CQ={cq} CK={ck} indexed={indexed}")
+    announce(f"H={h} N={video} CQ={cq} CK={ck} D={d} indexed={indexed}")
     q, k, v, qidx, kidx = (t.to(DEV) for t in (q, k, v, qidx, kidx))
     args = (qc.to(DEV), kc.to(DEV), qs.to(DEV), ks.to(DEV), 1e-9, 100)
     emap, eqs, eks, kept = clustering_cuda.select_connections(*args, text=(valid, text), with_kept=True)
     work = clustering_cuda.select_work(*args, (valid, text), length, length)
+    if check_items:
+        # The items against the map (the segment lists are checked on smaller shapes above).
+        counts, items = (t.cpu().numpy() for t in work.items())
+        lengths = work.row_lengths().cpu().numpy()
+        qsz = eqs.cpu().numpy().reshape(work.bh, work.rows)
+        for b in range(work.bh):
+            want = _expected_items(qsz[b], lengths[b], length)
+            assert [tuple(int(x) for x in it) for it in items[b, :counts[b]]] == want
     kw = dict(out_index=qidx, out_index_rows=video)
     if indexed:
         ref = attention_cuda.sparse_attention_indexed(q, k, v, emap, eqs, eks, qidx, kidx, video,
@@ -258,3 +262,26 @@ def test_persistent_grid_equals_map_attention(announce, indexed):
         torch.cuda.synchronize()
         assert torch.equal(out, ref)
         assert not work.queues().cpu().any()
+    return work
+
+
+@pytest.mark.parametrize("indexed", [True, False])
+def test_persistent_grid_equals_map_attention(announce, indexed):
+    """A launch with at least 8 item slots per resident workgroup (16 heads x 32896 rows, 130 x
+    514 extended map: 387 slots per head) runs the persistent grid, whose workgroups take items
+    from one queue per XCD; it must equal the map-driven attention (one workgroup per item) bit
+    for bit, twice on one work list (the first call resets the queues for the second)."""
+    _persistent_case(announce, 7 + indexed, 16, 128, 512, 32640, 256, 200, 64, indexed, False)
+
+
+@pytest.mark.parametrize("indexed,d", [(True, 128), (False, 128), (True, 64)])
+def test_long_sequence_items_on_eight_wave_workgroups(announce, indexed, d):
+    """At 65536 query rows and more, query clusters are cut into items of 256 rows, run by
+    8-wavefront workgroups (4 heads x 65856 rows, 130 x 514 extended map): the items follow the
+    map, and the persistent grid over them equals the one-workgroup-per-item grid of the
+    map-driven attention bit for bit (items of up to 128 rows pair their waves over the two key
+    halves of every tile, longer ones give each wave its own 32-row block)."""
+    work = _persistent_case(announce, 11 + indexed + d, 4, 128, 512, 65600, 256, 200, d, indexed, True)
+    counts, items = (t.cpu().numpy() for t in work.items())
+    rows = np.concatenate([items[b, :counts[b], 2] for b in range(work.bh)])
+    assert rows.max() == 256 and (rows <= 128).any() and ((rows > 128) & (rows < 256)).any()
