@@ -723,7 +723,7 @@ __device__ __forceinline__ void attention_item(
 #pragma unroll
         for (int r0 = 0; r0 < H; r0 += 2) {
             const bool turn = rb >= r0 && rb < r0 + 2;
-            float* xch = reinterpret_cast<float*>(&kvs[0][0]) + ((rb - r0) * kWave + lane) * (NB * 16 + 2);
+            float* xch = reinterpret_cast<float*>(&kvs[0][0]) + ((turn ? rb - r0 : 0) * kWave + lane) * (NB * 16 + 2);
             if (turn && hb == 1 && wave_active) {
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb)
