@@ -201,7 +201,9 @@ size_t peco_select_work_size(int bh, int sq, int cq, int ck, int extend);
  * attention's item queue counters: both zero before the first call on a buffer (allocate it
  * zeroed), and every selection (arrival counters) and attention (queue counters) call leaves
  * them zero, so one buffer serves calls ordered on a stream but not overlapping calls. sq and
- * sk are the attention's query and key lengths (video + text). */
+ * sk are the attention's query and key lengths (video + text). An item holds at most 128
+ * query rows, 256 when sq is 65536 or more (the attention then runs 8-wavefront workgroups);
+ * the rule depends on sq alone, which the attention call must repeat. */
 int peco_select_work(const float* qc, const float* kc, const int32_t* q_counts, const int32_t* k_counts, int bh,
                      int cq, int ck, int dims, float p, int minimum, int extend, int valid_text, int text, int sq,
                      int sk, uint8_t* map, int32_t* ext_q, int32_t* ext_k, int32_t* work, size_t work_ints,
