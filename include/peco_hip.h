@@ -72,9 +72,9 @@ int peco_cluster_sort(const int32_t* labels, int batch, int tokens, int clusters
                       int32_t* counts, int32_t* offsets, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Fused Lloyd fit (peco/clustering.py:17-89 with tol=0) of num_problems (1 or 2)
- * independent problems; with two, the second runs on a library-owned stream of the current
- * device, forked from `stream` and joined back to it with events, so the call is ordered on
- * `stream` like a single chain. Problem i: x[i] rows [batch, tokens, dims]
+ * independent problems. The problems' batch entries run as four chains of launches, three of
+ * them on library-owned streams of the current device, forked from `stream` and joined back to
+ * it with events, so the call is ordered on `stream` like a single chain. Problem i: x[i] rows [batch, tokens, dims]
  * in `dtype` with batch stride x_batch_stride[i] elements (NULL or 0 = tokens*dims),
  * initial centres centers_in[i] fp32 [batch, clusters, dims]; outputs centers_out[i],
  * labels[i] [batch,tokens], counts[i] [batch,clusters], sorted_indices[i] (stable sort

@@ -131,8 +131,8 @@ class KMeansProblem:
 
 
 def kmeans_fit(problems, iterations, pack=None, pack_order="cluster"):
-    """Fused Lloyd fit of one or two problems (two run as two chains of launches, the second
-    on a library stream forked from and joined back to the current stream).
+    """Fused Lloyd fit of one or two problems (their heads run as four chains of launches, three
+    on library streams forked from and joined back to the current stream).
 
     Returns, per problem, (labels int32 [B,N], centers fp32 [B,K,D], counts int32 [B,K],
     indices int32 [B,N], offsets int32 [B,K+1]); indices is the stable sort of labels.

@@ -24,8 +24,8 @@
 // Per iteration: assign (+ per-tile label histogram via global atomics) -> sort scan ->
 // sort place (stable counting sort, also yields the final permutation for stage 3) ->
 // update (sequential per-cluster sums in token order; also prepares the next iteration's
-// split-bf16 centres and canonical norms). Two problems (Q and K) run as two chains of launches
-// on two streams (km_fit_two_chains), or share every launch when no second stream is available.
+// split-bf16 centres and canonical norms). The problems' heads run as four chains of launches
+// on four streams (km_fit_chains), or share every launch when no side stream is available.
 #include "base_offset.hpp"
 #include "common.hpp"
 #include "sort.hpp"
@@ -1316,23 +1316,30 @@ size_t km_workspace_raw(int batch, int tokens, int clusters, int dims) {
     return bytes;
 }
 
-// Workspace (bytes) for one problem: its buffers plus slack for the fit's halves, whose
-// buffers are rounded up separately (at most 64 bytes more per buffer).
+// Workspace (bytes) for one problem: its buffers plus slack for the fit's chains, whose parts
+// of the buffers are rounded up separately (at most 64 bytes more per buffer and extra part).
 size_t km_workspace_bytes(int batch, int tokens, int clusters, int dims) {
-    return km_workspace_raw(batch, tokens, clusters, dims) + 64 * 16;
+    return km_workspace_raw(batch, tokens, clusters, dims) + 64 * 32;
 }
 
-// A fit runs as up to four chains of launches: each problem's batch entries (heads) in two
-// halves, one chain on the caller's stream and the others on library-owned streams of the
-// current device (default priority), forked from the caller's stream with one event and
-// joined back to it with one event per side stream. One problem's memory-bound launches and
-// another's MFMA-bound ones then overlap and the launches' tails interleave: the 480p Q+K
-// fit takes 0.65-0.66 ms this way, 0.69-0.70 ms as two chains (one per problem) and 0.72 ms
-// with both problems sharing every launch. The streams and events are created once per
-// device; the mutex keeps one fork-join at a time per process on the host. If the streams
+// A fit runs as four chains of launches, one on the caller's stream and the others on
+// library-owned streams of the current device (default priority), forked from the caller's
+// stream with one event and joined back to it with one event per side stream. Two layouts:
+//   - by problem: each problem's batch entries (heads) in two halves, one problem per chain.
+//     One problem's memory-bound launches and another's MFMA-bound ones overlap and the
+//     launches' tails interleave: the 544p Q+K fit 3.46-3.47 ms, against 3.54-3.56 ms mixed;
+//   - mixed, for two problems of at most kMixedTokens tokens (the 480p layer): each chain
+//     takes a quarter of both problems' heads, sharing its launches (larger-K assign blocks
+//     first), so the four chains carry equal work and end together: the 480p layer 1.089-1.091
+//     against 1.104-1.111 ms by problem (fit 0.617-0.632 against 0.625-0.646 ms).
+// More chains than the process's four hardware queues serialize (the 480p fit 0.92 ms with six
+// or eight), and at 720p the layouts are within 1%. The streams and events are created once
+// per device; the mutex keeps one fork-join at a time per process on the host. If the streams
 // cannot be made, the problems share launches instead.
-constexpr int kFitParts = 2;                    // chains per problem (batch halves)
-constexpr int kSideStreams = kMaxKm * kFitParts - 1;
+constexpr int kFitChains = 4;
+constexpr int kFitParts = 2;                    // chains per problem in the by-problem layout
+constexpr int kMixedTokens = 16384;
+constexpr int kSideStreams = kFitChains - 1;
 
 struct SideStream {
     hipStream_t stream = nullptr;
@@ -1387,40 +1394,63 @@ KmFitDesc slice_desc(const KmFitDesc& d, int b0, int nb, int dims, int dtype) {
 hipError_t km_fit_launches(const KmFitDesc* descs, int num, int dims, int dtype, int iterations, void* workspace,
                            float* sums, hipStream_t stream);
 
-// The chains of a fit (see above). The workspace holds each problem's slice of
-// km_workspace_bytes in turn; the halves of a problem take their parts of it in order (a
-// problem's size includes the slack for the extra rounding of two parts).
+// The chains of a fit (see above). By problem, the workspace holds each problem's slice of
+// km_workspace_bytes in turn and the halves of a problem take their parts of it in order;
+// mixed, the chains take their parts one after another. (A problem's size includes the slack
+// for the extra rounding of up to kFitChains parts.)
 hipError_t km_fit_chains(const KmFitDesc* descs, int num, int dims, int dtype, int iterations, void* workspace,
                          hipStream_t stream, const SideStream (&side)[kSideStreams], std::mutex& m) {
     std::lock_guard<std::mutex> lock(m);
-    KmFitDesc parts[kMaxKm * kFitParts];
-    char* wsp[kMaxKm * kFitParts];
-    int n = 0;
+    KmFitDesc parts[kFitChains][kMaxKm];
+    int nparts[kFitChains];
+    char* wsp[kFitChains];
+    bool mixed = num == 2;
+    for (int q = 0; q < num; ++q) mixed = mixed && descs[q].tokens <= kMixedTokens && descs[q].batch >= kFitChains;
     char* ws = static_cast<char*>(workspace);
-    for (int q = 0; q < num; ++q) {
-        const KmFitDesc& d = descs[q];
-        char* w = ws;
-        for (int i = 0; i < kFitParts; ++i) {
-            const int b0 = d.batch * i / kFitParts, b1 = d.batch * (i + 1) / kFitParts;
-            parts[n] = slice_desc(d, b0, b1 - b0, dims, dtype);
-            wsp[n++] = w;
-            w += km_workspace_raw(b1 - b0, d.tokens, d.clusters, dims);
+    int home;
+    if (mixed) {
+        for (int c = 0; c < kFitChains; ++c) {
+            wsp[c] = ws;
+            nparts[c] = num;
+            for (int q = 0; q < num; ++q) {
+                const KmFitDesc& d = descs[q];
+                const int b0 = d.batch * c / kFitChains, b1 = d.batch * (c + 1) / kFitChains;
+                parts[c][q] = slice_desc(d, b0, b1 - b0, dims, dtype);
+                ws += km_workspace_raw(b1 - b0, d.tokens, d.clusters, dims);
+            }
         }
-        ws += km_workspace_bytes(d.batch, d.tokens, d.clusters, dims);
+        home = 0;
+    } else {
+        int n = 0;
+        for (int q = 0; q < num; ++q) {
+            const KmFitDesc& d = descs[q];
+            char* w = ws;
+            for (int i = 0; i < kFitParts; ++i, ++n) {
+                const int b0 = d.batch * i / kFitParts, b1 = d.batch * (i + 1) / kFitParts;
+                parts[n][0] = slice_desc(d, b0, b1 - b0, dims, dtype);
+                nparts[n] = 1;
+                wsp[n] = w;
+                w += km_workspace_raw(b1 - b0, d.tokens, d.clusters, dims);
+            }
+            ws += km_workspace_bytes(d.batch, d.tokens, d.clusters, dims);
+        }
+        for (int c = n; c < kFitChains; ++c) nparts[c] = 0;
+        // The first half of the last problem (the larger one in the layer) on the caller's stream.
+        home = (num - 1) * kFitParts;
     }
-    // The first half of the last problem (the larger one in the layer) on the caller's stream.
-    const int home = (num - 1) * kFitParts;
     hipError_t e = hipEventRecord(side[0].fork, stream);
-    for (int i = 0; e == hipSuccess && i < n - 1; ++i) e = hipStreamWaitEvent(side[i].stream, side[0].fork, 0);
+    for (int i = 0; e == hipSuccess && i < kSideStreams; ++i) e = hipStreamWaitEvent(side[i].stream, side[0].fork, 0);
     int si = 0;
-    for (int i = 0; e == hipSuccess && i < n; ++i) {
-        if (i == home) continue;
-        e = km_fit_launches(&parts[i], 1, dims, dtype, iterations, wsp[i], nullptr, side[si].stream);
+    for (int c = 0; e == hipSuccess && c < kFitChains; ++c) {
+        if (c == home) continue;
+        if (nparts[c] > 0) e = km_fit_launches(parts[c], nparts[c], dims, dtype, iterations, wsp[c], nullptr,
+                                               side[si].stream);
         if (e == hipSuccess) e = hipEventRecord(side[si].join, side[si].stream);
         ++si;
     }
-    if (e == hipSuccess) e = km_fit_launches(&parts[home], 1, dims, dtype, iterations, wsp[home], nullptr, stream);
-    for (int i = 0; e == hipSuccess && i < n - 1; ++i) e = hipStreamWaitEvent(stream, side[i].join, 0);
+    if (e == hipSuccess) e = km_fit_launches(parts[home], nparts[home], dims, dtype, iterations, wsp[home], nullptr,
+                                             stream);
+    for (int i = 0; e == hipSuccess && i < kSideStreams; ++i) e = hipStreamWaitEvent(stream, side[i].join, 0);
     return e;
 }
 

@@ -1,7 +1,9 @@
-"""The two-problem fit runs its second problem on a library stream forked from and joined back
-to the caller's stream. Its results must not depend on which stream the caller is on, on
-calls queued back to back without a synchronization, or on work the caller queues right
-after the call on its own stream."""
+"""The fit runs as four chains of launches, three on library streams forked from and joined back
+to the caller's stream: by problem (each problem's heads in halves) or, for two problems of at
+most 16384 tokens with at least four heads, mixed (each chain a quarter of both problems'
+heads). Its results must not depend on the layout, on which stream the caller is on, on calls
+queued back to back without a synchronization, or on work the caller queues right after the
+call on its own stream."""
 import pytest
 import torch
 
@@ -30,9 +32,15 @@ def _equal(a, b):
     return all(torch.equal(x, y) for pa, pb in zip(a, b) for x, y in zip(pa, pb))
 
 
-def test_fit_on_a_caller_stream_matches_the_default_stream(announce):
-    announce("two-problem fit on a caller stream, consumer on the same stream")
-    problems = _problems(1)
+# Three heads: the by-problem layout; six heads (at most 16384 tokens): the mixed one; 17000
+# tokens: by problem again.
+LAYOUTS = [(3, 5000), (6, 3000), (4, 17000)]
+
+
+@pytest.mark.parametrize("h,n", LAYOUTS)
+def test_fit_on_a_caller_stream_matches_the_default_stream(announce, h, n):
+    announce(f"two-problem fit on a caller stream, consumer on the same stream, H={h} N={n}")
+    problems = _problems(1, h=h, n=n)
     ref = clustering_cuda.kmeans_fit(problems, 4)
     torch.cuda.synchronize()
     s = torch.cuda.Stream(device=DEV)
@@ -44,8 +52,19 @@ def test_fit_on_a_caller_stream_matches_the_default_stream(announce):
         cent = out[1][1].clone()
     s.synchronize()
     assert _equal(ref, out)
-    assert total.item() == 2 * 3 * 5000  # every token counted once per problem
+    assert total.item() == 2 * h * n  # every token counted once per problem
     assert torch.equal(cent, ref[1][1])
+
+
+@pytest.mark.parametrize("h,n", LAYOUTS[:2])
+def test_layouts_match_one_problem_fits(announce, h, n):
+    """Each problem fitted alone (its heads in halves) equals its part of the two-problem fit."""
+    announce(f"two-problem fit against one-problem fits, H={h} N={n}")
+    problems = _problems(2, h=h, n=n)
+    both = clustering_cuda.kmeans_fit(problems, 3)
+    alone = [clustering_cuda.kmeans_fit([p], 3)[0] for p in problems]
+    torch.cuda.synchronize()
+    assert _equal(both, alone)
 
 
 def test_fits_queued_back_to_back(announce):
