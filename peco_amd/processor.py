@@ -157,7 +157,7 @@ class PecoAttention:
         (peco/processor.py:97-113).
 
         query/key are the video parts [B,H,N,D]; returns (q_labels, k_labels, q_sizes, k_sizes)
-        with sizes [B,H,K]. Both fits run in one library call (two chains of launches).
+        with sizes [B,H,K]. Both fits run in one library call (four chains of launches).
         """
         fit = self._fit_clusters(query, key)
         return fit.q_labels, fit.k_labels, fit.q_sizes, fit.k_sizes
