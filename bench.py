@@ -403,9 +403,9 @@ def run_sequence(workload, steps, warmup):
 
 def measure(name, steps, warmup, stage_reps):
     """One workload's layer: ms per step, stage times, realised F4 and the attention roofline
-    (the attention launch's average duration over the timed steps, from events recorded on its
-    stream around each launch)."""
-    from peco_amd import attention_cuda, workloads
+    (the attention launch's average duration over the timed steps, from HIP timing events recorded
+    on its stream immediately around each launch, created without the system-scope fence)."""
+    from peco_amd import _native, attention_cuda, workloads
 
     dev = torch.device("cuda:0")
     wl = workloads.make_workload(name, device=dev)
@@ -417,7 +417,7 @@ def measure(name, steps, warmup, stage_reps):
         for _ in range(warmup):
             run_step(layer, wl, q, k, v, q_init, k_init)
         torch.cuda.synchronize()
-        launches = attention_cuda.launch_events = []
+        timer = attention_cuda.launch_timer = _native.LaunchTimer()
         try:
             t0 = time.perf_counter()
             for _ in range(steps):
@@ -425,10 +425,11 @@ def measure(name, steps, warmup, stage_reps):
             torch.cuda.synchronize()
             ms = (time.perf_counter() - t0) * 1e3 / steps
         finally:
-            attention_cuda.launch_events = None
-        if not launches:
+            attention_cuda.launch_timer = None
+        if not len(timer):
             raise RuntimeError("the layer step ran no work-list attention launch to time")
-        t_attn = sum(a.elapsed_time(b) for a, b in launches) / len(launches)
+        launches = timer.elapsed_ms()
+        t_attn = sum(launches) / len(launches)
         stages, flops, attn_args = stage_breakdown(layer, wl, q, k, v, q_init, k_init, stage_reps)
     value = flops / (ms * 1e-3) / 1e12
     achieved = flops / (t_attn * 1e-3) / 1e12

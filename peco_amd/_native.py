@@ -183,6 +183,67 @@ def current_stream(device, *tensors) -> ctypes.c_void_p:
     return ctypes.c_void_p(stream.cuda_stream)
 
 
+# hipEventDisableSystemFence (hip_runtime_api.h): the event skips the system-scope cache writeback
+# and invalidation of a default event when it is recorded.
+HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000
+
+
+class LaunchTimer:
+    """Timing events recorded in pairs immediately around kernel launches, for measurement.
+
+    They are HIP events created with hipEventDisableSystemFence, which the HIP runtime documents
+    for events used only to measure time: recording one then performs no system-scope cache
+    writeback and invalidation, so the timer perturbs the work it times less than a default
+    event does. The HIP entry points are resolved through this library's own dependency (the
+    runtime torch has loaded). Read the durations after a device synchronize.
+    """
+
+    def __init__(self):
+        lib = library()
+        self._create = lib.hipEventCreateWithFlags
+        self._create.argtypes, self._create.restype = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint], ctypes.c_int
+        self._record = lib.hipEventRecord
+        self._record.argtypes, self._record.restype = [ctypes.c_void_p, ctypes.c_void_p], ctypes.c_int
+        self._elapsed = lib.hipEventElapsedTime
+        self._elapsed.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self._elapsed.restype = ctypes.c_int
+        self._destroy = lib.hipEventDestroy
+        self._destroy.argtypes, self._destroy.restype = [ctypes.c_void_p], ctypes.c_int
+        self._pairs = []
+        self._open = None
+
+    def _event(self, stream):
+        event = ctypes.c_void_p()
+        if self._create(ctypes.byref(event), HIP_EVENT_DISABLE_SYSTEM_FENCE) != 0:
+            raise RuntimeError("hipEventCreateWithFlags failed")
+        if self._record(event, stream) != 0:
+            raise RuntimeError("hipEventRecord failed")
+        return event
+
+    def start(self, stream):
+        self._open = self._event(stream)
+
+    def stop(self, stream):
+        self._pairs.append((self._open, self._event(stream)))
+        self._open = None
+
+    def __len__(self):
+        return len(self._pairs)
+
+    def elapsed_ms(self):
+        """The recorded pairs' durations in ms (the events are released)."""
+        out = []
+        for start, end in self._pairs:
+            ms = ctypes.c_float()
+            if self._elapsed(ctypes.byref(ms), start, end) != 0:
+                raise RuntimeError("hipEventElapsedTime failed")
+            out.append(ms.value)
+            self._destroy(start)
+            self._destroy(end)
+        self._pairs = []
+        return out
+
+
 DTYPE_CODES = {}
 
 

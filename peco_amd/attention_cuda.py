@@ -12,10 +12,10 @@ import torch
 
 from . import _native
 
-# Per-launch timing of the work-list attention (for measurement): None, or a list to which
-# every sparse_attention_work call appends a (start, end) pair of timing events recorded on
-# its stream immediately around the kernel launch.
-launch_events = None
+# Per-launch timing of the work-list attention (for measurement): None, or an object whose
+# start(stream) and stop(stream) every sparse_attention_work call invokes immediately around
+# its kernel launch (such as _native.LaunchTimer, which records HIP timing events there).
+launch_timer = None
 
 
 def _device_is_gfx950(device) -> bool:
@@ -242,18 +242,16 @@ def sparse_attention_work(
             raise RuntimeError("This HIP build requires an MI355X-class gfx950 GPU")
         library = _native.library()
         stream = _native.current_stream(q.device, q, k, v, work.buffer, out_index, k_index, q_centroids)
-        events = launch_events
-        if events is not None:
-            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            start.record()
+        timer = launch_timer
+        if timer is not None:
+            timer.start(stream)
         error = library.peco_sparse_attention_work(
             _native.ptr(q), _native.ptr(k), _native.ptr(v), _native.ptr(output), _native.ptr(out_index), rows,
             _native.ptr(k_index), _native.ptr(q_centroids), q_clusters, int(bits) if q_centroids is not None else 0,
             _native.ptr(work.buffer), work.ints, batch * heads, sq, sk, dim, work.rows, work.cols,
             0 if q.dtype == torch.float16 else 1, stream)
-        if events is not None:
-            end.record()
-            events.append((start, end))
+        if timer is not None:
+            timer.stop(stream)
         if error:
             message = library.peco_attention_error_string(error).decode("utf-8", errors="replace")
             raise RuntimeError(f"PECO HIP sparse attention launch failed: {message} ({error})")
