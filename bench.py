@@ -91,7 +91,7 @@ def stage_breakdown(layer, wl, q, k, v, q_init, k_init, reps):
     so the host's launch work overlaps the device's; the first repetition, which starts on
     an idle device, is not counted.
     """
-    from peco_amd import clustering_cuda, workloads
+    from peco_amd import _native, clustering_cuda, workloads
 
     s = wl.shape
     n, dim, heads = s.video, s.dims, s.heads
@@ -100,7 +100,7 @@ def stage_breakdown(layer, wl, q, k, v, q_init, k_init, reps):
     length = q.shape[2]
     events = []
     for _ in range(reps + 1):
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+        ev = [_native.FencelessEvent() for _ in range(len(names) + 1)]
         ev[0].record()
         layer.q_centroids, layer.k_centroids = q_init, k_init
         fit = layer._fit_clusters(q[:, :, :n], k[:, :, :n], pack_keys=(s.bits, k, None) if s.bits else None,
@@ -143,10 +143,12 @@ def run_attention(args_):
 
 def attention_kernel_time(args_, reps=20):
     """Average duration of the sparse-attention launch on its stream."""
+    from peco_amd import _native
+
     for _ in range(3):
         run_attention(args_)
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start, end = _native.FencelessEvent(), _native.FencelessEvent()
     start.record()
     for _ in range(reps):
         run_attention(args_)
@@ -263,7 +265,7 @@ def profile_target(args):
         # (Base-Offset workloads), each args.reps times after two untimed calls.
         print(json.dumps(measure_integer_scores(args.workload, 1, 1, args.reps)), flush=True)
         return
-    from peco_amd import clustering_cuda, workloads
+    from peco_amd import _native, clustering_cuda, workloads
 
     wl = workloads.make_workload(args.workload, device=dev)
     s = wl.shape
@@ -276,7 +278,7 @@ def profile_target(args):
                         clustering_cuda.KMeansProblem(wl.key[0, :, :n], wl.k_init)]
             clustering_cuda.kmeans_fit(problems, s.iterations)
             torch.cuda.synchronize()
-            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start, end = _native.FencelessEvent(), _native.FencelessEvent()
             start.record()
             for _ in range(args.reps):
                 clustering_cuda.kmeans_fit(problems, s.iterations)
@@ -296,7 +298,7 @@ def profile_target(args):
                          [layer.q_centroids, layer.k_centroids, None], [s.bits, s.bits, 0], n)
             clustering_cuda.pack_clustered(*pack_args)
             torch.cuda.synchronize()
-            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start, end = _native.FencelessEvent(), _native.FencelessEvent()
             start.record()
             for _ in range(args.reps):
                 clustering_cuda.pack_clustered(*pack_args)
@@ -325,7 +327,7 @@ def run_sequence(workload, steps, warmup):
     as PecoAttention.attention does across denoising steps (peco/processor.py:98-113). All
     inputs are generated before timing. value = sum of the calls' F4 / sequence time.
     """
-    from peco_amd import clustering_cuda, processor, workloads
+    from peco_amd import _native, clustering_cuda, processor, workloads
 
     dev = torch.device("cuda:0")
     wl = workloads.make_workload(workload, device=dev)
@@ -342,7 +344,7 @@ def run_sequence(workload, steps, warmup):
         outs = []
         for i, cur in enumerate(inputs):
             if times is not None:
-                ev = torch.cuda.Event(enable_timing=True)
+                ev = _native.FencelessEvent()
                 ev.record()
                 times.append(ev)
             if i == 0:
@@ -352,7 +354,7 @@ def run_sequence(workload, steps, warmup):
                 layer.config = warm_cfg
             outs.append(layer.attention(cur.query, cur.key, cur.value))
         if times is not None:
-            ev = torch.cuda.Event(enable_timing=True)
+            ev = _native.FencelessEvent()
             ev.record()
             times.append(ev)
         return outs
@@ -459,7 +461,7 @@ def measure_integer_scores(name, steps, warmup, reps):
     """The Base-Offset layer with integer scores (PecoAttention.integer_scores, an extension
     with no counterpart in the reference): ms per layer step, and the integer-score attention
     launch against the launch over rounded reconstructions on the same selection."""
-    from peco_amd import attention_cuda, clustering_cuda, workloads
+    from peco_amd import _native, attention_cuda, clustering_cuda, workloads
 
     wl = workloads.make_workload(name, device=torch.device("cuda:0"))
     s = wl.shape
@@ -503,7 +505,7 @@ def measure_integer_scores(name, steps, warmup, reps):
             for _ in range(2):
                 fn()
             torch.cuda.synchronize()
-            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start, end = _native.FencelessEvent(), _native.FencelessEvent()
             start.record()
             for _ in range(reps):
                 fn()

@@ -188,43 +188,77 @@ def current_stream(device, *tensors) -> ctypes.c_void_p:
 HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000
 
 
-class LaunchTimer:
-    """Timing events recorded in pairs immediately around kernel launches, for measurement.
-
-    They are HIP events created with hipEventDisableSystemFence, which the HIP runtime documents
-    for events used only to measure time: recording one then performs no system-scope cache
-    writeback and invalidation, so the timer perturbs the work it times less than a default
-    event does. The HIP entry points are resolved through this library's own dependency (the
-    runtime torch has loaded). Read the durations after a device synchronize.
-    """
+class _HipEvents:
+    """hipEventCreateWithFlags / Record / ElapsedTime / Destroy, resolved through this library's
+    own dependency on the HIP runtime (the one torch has loaded)."""
 
     def __init__(self):
         lib = library()
-        self._create = lib.hipEventCreateWithFlags
-        self._create.argtypes, self._create.restype = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint], ctypes.c_int
-        self._record = lib.hipEventRecord
-        self._record.argtypes, self._record.restype = [ctypes.c_void_p, ctypes.c_void_p], ctypes.c_int
-        self._elapsed = lib.hipEventElapsedTime
-        self._elapsed.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
-        self._elapsed.restype = ctypes.c_int
-        self._destroy = lib.hipEventDestroy
-        self._destroy.argtypes, self._destroy.restype = [ctypes.c_void_p], ctypes.c_int
+        self.create = lib.hipEventCreateWithFlags
+        self.create.argtypes, self.create.restype = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint], ctypes.c_int
+        self.record = lib.hipEventRecord
+        self.record.argtypes, self.record.restype = [ctypes.c_void_p, ctypes.c_void_p], ctypes.c_int
+        self.elapsed = lib.hipEventElapsedTime
+        self.elapsed.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.elapsed.restype = ctypes.c_int
+        self.destroy = lib.hipEventDestroy
+        self.destroy.argtypes, self.destroy.restype = [ctypes.c_void_p], ctypes.c_int
+
+
+_HIP_EVENTS = None
+
+
+class FencelessEvent:
+    """A HIP timing event created with hipEventDisableSystemFence, with the record/elapsed_time
+    interface of torch.cuda.Event. The HIP runtime documents the flag for events used only to
+    measure time: recording one performs no system-scope cache writeback and invalidation, so it
+    perturbs the work it times less than a default event does. Read it after a synchronize."""
+
+    def __init__(self):
+        global _HIP_EVENTS
+        if _HIP_EVENTS is None:
+            _HIP_EVENTS = _HipEvents()
+        self._api = _HIP_EVENTS
+        self._event = ctypes.c_void_p()
+        if self._api.create(ctypes.byref(self._event), HIP_EVENT_DISABLE_SYSTEM_FENCE) != 0:
+            raise RuntimeError("hipEventCreateWithFlags failed")
+
+    def record(self, stream=None):
+        """Record on `stream` (a hipStream_t), by default torch's current stream."""
+        if stream is None:
+            import torch
+
+            stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        if self._api.record(self._event, stream) != 0:
+            raise RuntimeError("hipEventRecord failed")
+
+    def elapsed_time(self, end):
+        ms = ctypes.c_float()
+        if self._api.elapsed(ctypes.byref(ms), self._event, end._event) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value
+
+    def __del__(self):
+        if getattr(self, "_event", None) and self._event.value:
+            self._api.destroy(self._event)
+
+
+class LaunchTimer:
+    """FencelessEvent pairs recorded immediately around kernel launches, for measurement:
+    start(stream) and stop(stream) around each launch, then elapsed_ms() after a synchronize."""
+
+    def __init__(self):
         self._pairs = []
         self._open = None
 
-    def _event(self, stream):
-        event = ctypes.c_void_p()
-        if self._create(ctypes.byref(event), HIP_EVENT_DISABLE_SYSTEM_FENCE) != 0:
-            raise RuntimeError("hipEventCreateWithFlags failed")
-        if self._record(event, stream) != 0:
-            raise RuntimeError("hipEventRecord failed")
-        return event
-
     def start(self, stream):
-        self._open = self._event(stream)
+        self._open = FencelessEvent()
+        self._open.record(stream)
 
     def stop(self, stream):
-        self._pairs.append((self._open, self._event(stream)))
+        end = FencelessEvent()
+        end.record(stream)
+        self._pairs.append((self._open, end))
         self._open = None
 
     def __len__(self):
@@ -232,14 +266,7 @@ class LaunchTimer:
 
     def elapsed_ms(self):
         """The recorded pairs' durations in ms (the events are released)."""
-        out = []
-        for start, end in self._pairs:
-            ms = ctypes.c_float()
-            if self._elapsed(ctypes.byref(ms), start, end) != 0:
-                raise RuntimeError("hipEventElapsedTime failed")
-            out.append(ms.value)
-            self._destroy(start)
-            self._destroy(end)
+        out = [start.elapsed_time(end) for start, end in self._pairs]
         self._pairs = []
         return out
 
