@@ -325,9 +325,11 @@ def run_sequence(workload, steps, warmup):
     Call 0 fits from the seeded centroids with `iterations` Lloyd iterations; calls 1.. start
     from the layer's cached centroids with `warm_iterations` (PecoAttention's kmeans_iter_step),
     as PecoAttention.attention does across denoising steps (peco/processor.py:98-113). All
-    inputs are generated before timing. value = sum of the calls' F4 / sequence time.
+    inputs are generated before timing. value = sum of the calls' F4 / sequence time. The
+    roofline covers one more pass of the sequence with HIP events around each attention launch:
+    the calls' summed F4 over the launches' summed durations.
     """
-    from peco_amd import _native, clustering_cuda, processor, workloads
+    from peco_amd import _native, attention_cuda, clustering_cuda, processor, workloads
 
     dev = torch.device("cuda:0")
     wl = workloads.make_workload(workload, device=dev)
@@ -369,9 +371,16 @@ def run_sequence(workload, steps, warmup):
         torch.cuda.synchronize()
         ms = (time.perf_counter() - t0) * 1e3 / steps
         evs = []
-        sequence(evs)
-        torch.cuda.synchronize()
+        timer = attention_cuda.launch_timer = _native.LaunchTimer()
+        try:
+            sequence(evs)
+            torch.cuda.synchronize()
+        finally:
+            attention_cuda.launch_timer = None
         call_ms = [evs[i].elapsed_time(evs[i + 1]) for i in range(calls)]
+        launches = timer.elapsed_ms()
+        if len(launches) != calls:
+            raise RuntimeError(f"expected one attention launch per call, timed {len(launches)} for {calls} calls")
         # Realised F4 of every call: the same fits (bit-exact) rerun with the selection.
         flops = []
         n, dim = s.video, s.dims
@@ -387,6 +396,8 @@ def run_sequence(workload, steps, warmup):
             flops.append(workloads.attention_flops(emap, eqs, eks, dim))
     total = sum(flops)
     value = total / (ms * 1e-3) / 1e12
+    attn_ms = sum(launches)
+    achieved = total / (attn_ms * 1e-3) / 1e12
     line = {
         "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps,
         "warmup": warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
@@ -397,7 +408,13 @@ def run_sequence(workload, steps, warmup):
                    "keep_ratio": s.keep_ratio, "base_offset_bits": s.bits, "layer_calls_per_step": calls},
         "sequence": {"call_ms": [round(t, 4) for t in call_ms], "call_flops": flops,
                      "first_call_ms": round(call_ms[0], 4),
-                     "warm_call_ms": round(sum(call_ms[1:]) / max(1, calls - 1), 4)},
+                     "warm_call_ms": round(sum(call_ms[1:]) / max(1, calls - 1), 4),
+                     "attention_ms": [round(t, 4) for t in launches]},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic(s.name),
+                     "kernel": "sparse_attention_kernel, indexed inputs, work list from the selection launch; "
+                               "the calls' F4 over their launches' summed durations",
+                     "kernel_ms": round(attn_ms / calls, 4), "flops": total / calls},
         "layer_frac_of_peak": round(value / PEAK_BF16_TFLOPS, 4),
     }
     return line
