@@ -579,9 +579,8 @@ def main():
         torch.cuda.empty_cache()
         name, steps, warmup = SEQUENCE_WORKLOAD
         seq = run_sequence(name, steps, warmup)
-        others[name + "_sequence"] = {k_: v_ for k_, v_ in seq.items() if k_ not in line or k_ in ("value", "steps",
-                                                                                             "warmup", "ms_per_step",
-                                                                                             "config")}
+        keep = ("value", "steps", "warmup", "ms_per_step", "config", "roofline", "layer_frac_of_peak")
+        others[name + "_sequence"] = {k_: v_ for k_, v_ in seq.items() if k_ not in line or k_ in keep}
         line["other_workloads"] = others
     print(json.dumps(line), flush=True)
 
